@@ -1,0 +1,138 @@
+/*
+ * st_runtime.h - C ABI of the MI355X (gfx950) streaming-step backend, libstamd.so.
+ *
+ * This is the drop-in boundary for the reference's backend interface
+ * Stream::Runtime (include/Runtime.hpp:7-46). Plain pointers and sizes only; no C++
+ * types cross it. Every function returning int returns ST_OK (0) on success or a
+ * nonzero ST_ERR_* code and records a message readable with st_last_error() on the
+ * calling thread; this replaces the std::runtime_error the reference throws
+ * (src/cuda/Runtime.cu:178-194,285-287,399-425). A C++ shim that rethrows
+ * std::runtime_error(st_last_error()) restores the reference's exact interface.
+ *
+ * Threading: like the reference, a runtime is not thread-safe and has one outstanding
+ * command at a time (docs/transport.md:14); the calling thread does any polling.
+ */
+#ifndef ST_RUNTIME_H
+#define ST_RUNTIME_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  ST_OK = 0,
+  ST_ERR_INVALID = 1,   /* bad config, tensor, option or argument */
+  ST_ERR_DEVICE = 2,    /* HIP runtime failure or unsupported device */
+  ST_ERR_STATE = 3,     /* stopped runtime, exhausted sequence, worker exit, timeout */
+  ST_ERR_NUMERIC = 4    /* device-side watchdog (barrier timeout) tripped */
+};
+
+/* Stream::Backend (include/Runtime.hpp:7). CUDA = staged HIP kernels, GRAPH = the staged
+ * sequence captured in a hipGraph, FUSED = one cooperative launch per step, PERSISTENT =
+ * resident kernel driven through a host mailbox. CUBLAS / CUBLAS_GRAPH (vendor GEMV
+ * baselines) are not provided and are rejected with ST_ERR_INVALID. */
+enum {
+  ST_BACKEND_CUDA = 0,
+  ST_BACKEND_GRAPH = 1,
+  ST_BACKEND_CUBLAS = 2,
+  ST_BACKEND_CUBLAS_GRAPH = 3,
+  ST_BACKEND_FUSED = 4,
+  ST_BACKEND_PERSISTENT = 5
+};
+
+/* Weight storage. AS_MODEL = the checkpoint's own mode (FP32, or FP16 for a "mixed"
+ * checkpoint, src/cuda/Runtime.cu:231-246); BF16 = FP32 model whose weights are stored
+ * as bfloat16 (round to nearest even) with FP32 activations, K/V and reductions. */
+enum { ST_WEIGHTS_AS_MODEL = 0, ST_WEIGHTS_BF16 = 1 };
+
+/* = Stream::ModelConfig (include/Model.hpp:12-18), validated like
+ * ModelConfig::validate (src/runtime/Model.cpp:22-29). */
+typedef struct {
+  int32_t layers, width, heads, ffn, window, features;
+  float epsilon;
+} st_config;
+
+/* = Stream::RuntimeOptions (include/Runtime.hpp:8-19) plus weight_dtype.
+ * blocks: workgroups of 512 threads; 0 selects one per compute unit.
+ * vector_matvec and fused_attention are accepted for source compatibility; this
+ * backend always uses its wide-load matvec and LDS-staged attention. */
+typedef struct {
+  int32_t backend;
+  int32_t blocks;
+  int32_t backoff;
+  int32_t mapped;
+  int32_t vector_matvec;
+  int32_t fused_attention;
+  uint64_t max_events;
+  uint64_t initial_sequence;
+  double idle_seconds;
+  int32_t weight_dtype;
+  int32_t reserved;
+} st_options;
+
+/* One named host tensor, FP32 values, row-major [out, in]. Names and shapes follow the
+ * checkpoint manifest (reference/model.py:27-47; shape checks src/runtime/Model.cpp:120-139):
+ * "input" [width, features], "final_norm" [width], "score" [1, width], and per layer
+ * "layers.{l}.norm1|norm2" [width], ".q|k|v|out" [width, width], ".gate|up" [ffn, width],
+ * ".down" [width, ffn]. For a mixed model the values must be FP16-representable. */
+typedef struct {
+  const char* name;
+  int32_t rank;
+  int32_t shape[2];
+  const float* data;
+} st_tensor;
+
+typedef struct st_runtime st_runtime;
+
+/* Fill *options with the reference defaults (RuntimeOptions{}: GRAPH, 1 block, ... 30 s). */
+void st_options_default(st_options* options);
+
+/* Runtime(const Model&, RuntimeOptions) - src/cuda/Runtime.cu:169-292.
+ * mixed: 1 for a "mixed" checkpoint (FP16 weights, K/V and cast points). Tensors are
+ * copied; the caller may free them on return. */
+int st_runtime_create(const st_config* config, int32_t mixed, const st_tensor* tensors,
+                      size_t tensor_count, const st_options* options, st_runtime** out);
+
+/* ~Runtime() - stops and joins a persistent worker, frees device resources; never fails. */
+void st_runtime_destroy(st_runtime* runtime);
+
+/* float Runtime::step(const float* input) - src/cuda/Runtime.cu:430-455. Reads
+ * `features` floats, writes the score. */
+int st_runtime_step(st_runtime* runtime, const float* input, float* score);
+
+/* void Runtime::reset() - src/cuda/Runtime.cu:457-464. */
+int st_runtime_reset(st_runtime* runtime);
+
+/* void Runtime::stop() - src/cuda/Runtime.cu:466-474. Idempotent. */
+int st_runtime_stop(st_runtime* runtime);
+
+/* Snapshot Runtime::snapshot() - src/cuda/Runtime.cu:548-568. keys/values receive
+ * layers*width*window floats in [layer][head][slot][dim] order (FP16 cache decoded),
+ * hidden receives layers*width floats. Any output pointer may be NULL. */
+int st_runtime_snapshot(st_runtime* runtime, uint64_t* position, float* keys, float* values,
+                        float* hidden);
+
+/* double Runtime::deviceTrace(const float* inputs, size_t count) - src/cuda/Runtime.cu:596-630.
+ * Resets state, runs `count` events from a preloaded device copy and writes the mean
+ * microseconds per event. If per_event_us is not NULL it receives count per-event device
+ * durations (microseconds). */
+int st_runtime_device_trace(st_runtime* runtime, const float* inputs, size_t count,
+                            double* us_per_event, double* per_event_us);
+
+/* Json Runtime::info() const - src/cuda/Runtime.cu:570-594, as a JSON string. Writes at
+ * most cap bytes (NUL-terminated) and the full length to *needed. */
+int st_runtime_info_json(st_runtime* runtime, char* buffer, size_t cap, size_t* needed);
+
+/* Json probe() - src/cuda/Runtime.cu:134-161, as a JSON string. */
+int st_probe_json(char* buffer, size_t cap, size_t* needed);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* st_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,768 @@
+// Host runtime and C ABI of libstamd.so (see include/st_runtime.h).
+//
+// Owns the device state of one stream: a single weight arena laid out in phase order,
+// the K/V rings, an FP32 scratch arena, the device-held position and the grid-barrier
+// flags. Mirrors Stream::Runtime::Impl (src/cuda/Runtime.cu:167-653) behind a C ABI.
+#include "step_phases.hpp"
+#include "../../include/st_runtime.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+namespace stamd {
+
+static thread_local std::string g_last_error;
+
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+#define HIP_CHECK(expr)                                                                    \
+  do {                                                                                     \
+    hipError_t _e = (expr);                                                                \
+    if (_e != hipSuccess)                                                                  \
+      throw Error(ST_ERR_DEVICE, std::string(#expr) + ": " + hipGetErrorString(_e));       \
+  } while (0)
+
+// ---------------------------------------------------------------------------------------------
+// host-side rounding (round to nearest even), matching the device conversions
+
+static uint16_t host_half_bits(float value) {
+  uint32_t u;
+  std::memcpy(&u, &value, 4);
+  uint32_t sign = (u >> 16) & 0x8000u, exp = (u >> 23) & 0xffu, man = u & 0x7fffffu;
+  if (exp == 0xffu) return (uint16_t)(sign | 0x7c00u | (man ? (0x200u | (man >> 13)) : 0u));
+  int e = (int)exp - 127 + 15;
+  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {
+    if (e < -10) return (uint16_t)sign;
+    uint32_t full = man | 0x800000u;
+    int shift = 14 - e;
+    uint32_t half = full >> shift, rem = full & ((1u << shift) - 1u), mid = 1u << (shift - 1);
+    if (rem > mid || (rem == mid && (half & 1u))) half++;
+    return (uint16_t)(sign | half);
+  }
+  uint32_t half = ((uint32_t)e << 10) | (man >> 13), rem = man & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (half & 1u))) half++;
+  return (uint16_t)(sign | half);
+}
+
+static float host_half_to_float(uint16_t bits) {
+  uint32_t sign = ((uint32_t)bits & 0x8000u) << 16, exp = (bits >> 10) & 0x1fu, man = bits & 0x3ffu;
+  uint32_t u;
+  if (exp == 0x1fu) u = sign | 0x7f800000u | (man << 13);
+  else if (exp == 0) {
+    if (!man) u = sign;
+    else {
+      float f = (float)man * 5.9604644775390625e-8f;
+      return sign ? -f : f;
+    }
+  } else u = sign | ((exp + 112u) << 23) | (man << 13);
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+static uint16_t host_bf16_bits(float value) {
+  uint32_t u;
+  std::memcpy(&u, &value, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+static int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+// ---------------------------------------------------------------------------------------------
+
+struct DeviceBuffer {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  void alloc(size_t n) {
+    bytes = n;
+    HIP_CHECK(hipMalloc(&ptr, std::max<size_t>(n, 256)));
+  }
+  ~DeviceBuffer() {
+    if (ptr) (void)hipFree(ptr);
+  }
+};
+
+struct PinnedBuffer {
+  void* ptr = nullptr;
+  void alloc(size_t n) { HIP_CHECK(hipHostMalloc(&ptr, std::max<size_t>(n, 64), hipHostMallocDefault)); }
+  ~PinnedBuffer() {
+    if (ptr) (void)hipHostFree(ptr);
+  }
+};
+
+static void validate_config(const st_config& c) {
+  if (c.layers < 1 || c.layers > 16 || c.width < 1 || c.width > 1024 || c.heads < 1 ||
+      c.width % c.heads || (c.width / c.heads) % 2 || c.ffn < 1 || c.ffn > 4096 || c.window < 1 ||
+      c.window > 4096 || c.features < 1 || c.features > 1024 || !std::isfinite(c.epsilon) ||
+      c.epsilon <= 0)
+    throw Error(ST_ERR_INVALID, "Invalid or unsupported model dimensions");
+}
+
+static std::string json_escape(const std::string& s) {
+  std::string o;
+  for (char ch : s) {
+    if (ch == '"' || ch == '\\') o += '\\';
+    o += ch;
+  }
+  return o;
+}
+
+static std::string probe_json() {
+  int device = 0, driver = 0, runtime = 0;
+  HIP_CHECK(hipGetDevice(&device));
+  HIP_CHECK(hipDriverGetVersion(&driver));
+  HIP_CHECK(hipRuntimeGetVersion(&runtime));
+  hipDeviceProp_t p;
+  HIP_CHECK(hipGetDeviceProperties(&p, device));
+  int wall = 0, coop = 0;
+  HIP_CHECK(hipDeviceGetAttribute(&wall, hipDeviceAttributeWallClockRate, device));
+  HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device));
+  char bus[64] = {0};
+  (void)hipDeviceGetPCIBusId(bus, sizeof(bus), device);
+  std::ostringstream o;
+  o << "{\"gpu\": \"" << json_escape(p.name) << "\", \"arch\": \"" << json_escape(p.gcnArchName)
+    << "\", \"device\": " << device << ", \"compute_units\": " << p.multiProcessorCount
+    << ", \"lds_bytes_per_block\": " << p.sharedMemPerBlock
+    << ", \"global_bytes\": " << p.totalGlobalMem << ", \"l2_bytes\": " << p.l2CacheSize
+    << ", \"pci_bus\": \"" << bus << "\", \"clock_khz\": " << p.clockRate
+    << ", \"memory_clock_khz\": " << p.memoryClockRate << ", \"wall_clock_khz\": " << wall
+    << ", \"cooperative_launch\": " << coop << ", \"driver_version\": " << driver
+    << ", \"runtime_version\": " << runtime
+    << ", \"cpu_logical_count\": " << std::thread::hardware_concurrency() << "}";
+  return o.str();
+}
+
+// ---------------------------------------------------------------------------------------------
+
+class Runtime {
+ public:
+  Runtime(const st_config& config, bool mixed, const st_tensor* tensors, size_t count,
+          const st_options& options);
+  ~Runtime();
+  float step(const float* input);
+  void reset();
+  void stop();
+  void snapshot(uint64_t* position, float* keys, float* values, float* hidden);
+  double device_trace(const float* inputs, size_t count, double* per_event);
+  std::string info();
+
+ private:
+  void build_weights(const st_tensor* tensors, size_t count);
+  void launch_step();
+  void launch_phases();
+  void launch_fused();
+  template <int P> void launch_phases_t();
+  template <int P> void launch_fused_t();
+  template <int P> void launch_trace_t(const float* events, int count, unsigned long long* stamps);
+  template <int P> int legal_blocks_t();
+  void check_device_error();
+  void sync() { HIP_CHECK(hipStreamSynchronize(stream_)); }
+
+  st_config c_;
+  st_options opt_;
+  int prec_ = kFp32;
+  int dim_ = 0, grid_ = 1, legal_blocks_ = 1, cus_ = 1, wall_khz_ = 100000;
+  bool running_ = true;
+  hipStream_t stream_ = nullptr;
+  hipGraph_t graph_ = nullptr;
+  hipGraphExec_t graph_exec_ = nullptr;
+  DeviceBuffer weights_, keys_, values_, scratch_, counters_, position_, flags_, epoch_, rope_, args_dev_;
+  PinnedBuffer host_in_, host_out_;
+  StepArgs args_{};
+  const StepArgs* dargs_ = nullptr;
+  std::string probe_;
+};
+
+Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, size_t count,
+                 const st_options& options)
+    : c_(config), opt_(options) {
+  validate_config(c_);
+  if (options.idle_seconds <= 0 || options.idle_seconds > 3600 || options.blocks < 0)
+    throw Error(ST_ERR_INVALID, "Invalid blocks or idle budget");
+  if (options.initial_sequence >= std::numeric_limits<uint64_t>::max() - 1)
+    throw Error(ST_ERR_INVALID, "Initial sequence must leave room for RUN and STOP");
+  if (options.backend == ST_BACKEND_CUBLAS || options.backend == ST_BACKEND_CUBLAS_GRAPH)
+    throw Error(ST_ERR_INVALID, "Vendor-library backends are not provided by this build");
+  if (options.backend < 0 || options.backend > ST_BACKEND_PERSISTENT)
+    throw Error(ST_ERR_INVALID, "Unknown backend");
+  if (options.backend == ST_BACKEND_PERSISTENT)
+    throw Error(ST_ERR_INVALID, "Persistent backend not available in this build");
+  if (options.weight_dtype == ST_WEIGHTS_BF16 && mixed)
+    throw Error(ST_ERR_INVALID, "bfloat16 weight storage applies to FP32 checkpoints only");
+  if (options.weight_dtype != ST_WEIGHTS_AS_MODEL && options.weight_dtype != ST_WEIGHTS_BF16)
+    throw Error(ST_ERR_INVALID, "Unknown weight storage");
+  prec_ = mixed ? kMixed : (options.weight_dtype == ST_WEIGHTS_BF16 ? kBf16w : kFp32);
+  dim_ = c_.width / c_.heads;
+
+  probe_ = probe_json();
+  int device = 0;
+  HIP_CHECK(hipGetDevice(&device));
+  hipDeviceProp_t prop;
+  HIP_CHECK(hipGetDeviceProperties(&prop, device));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    throw Error(ST_ERR_DEVICE, std::string("Supported target is gfx950; found ") + prop.gcnArchName);
+  cus_ = prop.multiProcessorCount;
+  HIP_CHECK(hipDeviceGetAttribute(&wall_khz_, hipDeviceAttributeWallClockRate, device));
+  HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+
+  // ---- shape-derived layout
+  StepArgs& a = args_;
+  a.layers = c_.layers;
+  a.width = c_.width;
+  a.heads = c_.heads;
+  a.ffn = c_.ffn;
+  a.window = c_.window;
+  a.features = c_.features;
+  a.dim = dim_;
+  a.epsilon = c_.epsilon;
+  // Rows padded to whole 1 KiB slabs (zeros in weights and activations).
+  const int slab = 1024 / (prec_ == kFp32 ? 4 : 2);
+  a.width_p = round_up(c_.width, slab);
+  a.ffn_p = round_up(c_.ffn, slab);
+  a.features_p = round_up(c_.features, slab);
+  a.chunk = std::min(32, 2048 / dim_);
+  if (a.chunk < 1) a.chunk = 1;
+
+  build_weights(tensors, count);
+
+  // ---- state
+  const size_t kvb = prec_ == kMixed ? 2 : 4;
+  const size_t cache_elems = (size_t)c_.layers * c_.width * c_.window;
+  keys_.alloc(cache_elems * kvb);
+  values_.alloc(cache_elems * kvb);
+  a.keys = keys_.ptr;
+  a.values = values_.ptr;
+  a.cache_bytes = (uint32_t)(cache_elems * kvb);
+
+  int nch = (c_.window + a.chunk - 1) / a.chunk;
+  uint32_t off = 0;
+  auto take = [&](size_t n) {
+    uint32_t o = off;
+    off += (uint32_t)round_up((int)n, 64);
+    return o;
+  };
+  int vec = std::max({a.width_p, a.ffn_p, a.features_p});
+  a.s_input = take(a.features_p);
+  a.s_x = take(a.width_p);
+  a.s_q = take(a.width_p);
+  a.s_kcur = take(a.width_p);
+  a.s_vcur = take(a.width_p);
+  a.s_attn = take(a.width_p);
+  a.s_act = take(a.ffn_p);
+  a.s_hidden = take((size_t)c_.layers * c_.width);
+  a.s_score = take(64);
+  a.s_partial = take((size_t)c_.heads * nch * (dim_ + 2));
+  (void)vec;
+  scratch_.alloc((size_t)off * 4);
+  HIP_CHECK(hipMemset(scratch_.ptr, 0, (size_t)off * 4));
+  a.scratch = reinterpret_cast<float*>(scratch_.ptr);
+  a.scratch_bytes = off * 4;
+  a.error = reinterpret_cast<unsigned*>(a.scratch + a.s_score + 1);
+  a.input = a.scratch + a.s_input;
+
+  counters_.alloc((size_t)c_.heads * 32 * 4);
+  HIP_CHECK(hipMemset(counters_.ptr, 0, counters_.bytes));
+  a.head_count = reinterpret_cast<unsigned*>(counters_.ptr);
+  position_.alloc(8);
+  HIP_CHECK(hipMemset(position_.ptr, 0, 8));
+  a.position = reinterpret_cast<unsigned long long*>(position_.ptr);
+  flags_.alloc((size_t)kMaxGrid * kFlagStride * 4);
+  HIP_CHECK(hipMemset(flags_.ptr, 0, flags_.bytes));
+  a.flags = reinterpret_cast<unsigned*>(flags_.ptr);
+  epoch_.alloc(64);
+  HIP_CHECK(hipMemset(epoch_.ptr, 0, 64));
+  a.epoch = reinterpret_cast<unsigned*>(epoch_.ptr);
+
+  // RoPE inverse frequencies: powf(10000, -i/dim) for even i (src/cpu/Cpu.cpp:75).
+  std::vector<float> freq(dim_ / 2);
+  for (int j = 0; j < dim_ / 2; j++) freq[j] = std::pow(10000.0f, -(float)(2 * j) / (float)dim_);
+  rope_.alloc(freq.size() * 4);
+  HIP_CHECK(hipMemcpy(rope_.ptr, freq.data(), freq.size() * 4, hipMemcpyHostToDevice));
+  a.rope_freq = reinterpret_cast<const float*>(rope_.ptr);
+  a.spin_limit = (unsigned long long)wall_khz_ * 1000ull * 2ull;  // 2 s per barrier wait
+
+  host_in_.alloc((size_t)a.features_p * 4);
+  std::memset(host_in_.ptr, 0, (size_t)a.features_p * 4);
+  host_out_.alloc(64);
+
+  // ---- grid
+  switch (prec_) {
+    case kFp32: legal_blocks_ = legal_blocks_t<kFp32>(); break;
+    case kMixed: legal_blocks_ = legal_blocks_t<kMixed>(); break;
+    default: legal_blocks_ = legal_blocks_t<kBf16w>(); break;
+  }
+  grid_ = options.blocks == 0 ? std::min(cus_, kMaxGrid) : options.blocks;
+  if (grid_ > kMaxGrid) throw Error(ST_ERR_INVALID, "Requested grid exceeds the barrier capacity");
+  if (options.backend == ST_BACKEND_FUSED && grid_ > legal_blocks_)
+    throw Error(ST_ERR_INVALID,
+                "Requested cooperative grid exceeds actual occupancy limit " + std::to_string(legal_blocks_));
+  a.grid = grid_;
+  args_dev_.alloc(sizeof(StepArgs));
+  HIP_CHECK(hipMemcpy(args_dev_.ptr, &args_, sizeof(StepArgs), hipMemcpyHostToDevice));
+  dargs_ = reinterpret_cast<const StepArgs*>(args_dev_.ptr);
+
+  reset();
+  if (options.backend == ST_BACKEND_GRAPH) {
+    // Warm up outside capture, restore the initial state, then capture the phase sequence.
+    launch_phases();
+    sync();
+    reset();
+    HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    launch_phases();
+    HIP_CHECK(hipStreamEndCapture(stream_, &graph_));
+    HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+  }
+}
+
+Runtime::~Runtime() {
+  if (stream_) (void)hipStreamSynchronize(stream_);
+  if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+  if (graph_) (void)hipGraphDestroy(graph_);
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+template <int P>
+int Runtime::legal_blocks_t() {
+  int per_cu = 0;
+  HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_kernel<P>, kThreads, 0));
+  int trace_per_cu = 0;
+  HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&trace_per_cu, trace_kernel<P>, kThreads, 0));
+  return std::max(1, std::min(per_cu, trace_per_cu) * cus_);
+}
+
+// Weight arena in phase order: input, then per layer norm1, norm2, qkv (stacked q;k;v),
+// out, gateup (row 2i = gate i, row 2i+1 = up i), down; then final_norm, score.
+// Rows are padded with zeros to a multiple of 16 bytes.
+void Runtime::build_weights(const st_tensor* tensors, size_t count) {
+  std::map<std::string, const st_tensor*> byname;
+  for (size_t i = 0; i < count; i++) {
+    if (!tensors[i].name || !tensors[i].data) throw Error(ST_ERR_INVALID, "Null tensor");
+    if (!byname.emplace(tensors[i].name, &tensors[i]).second)
+      throw Error(ST_ERR_INVALID, std::string("Duplicate tensor: ") + tensors[i].name);
+  }
+  auto get = [&](const std::string& name, std::vector<int> shape) -> const st_tensor* {
+    auto it = byname.find(name);
+    if (it == byname.end()) throw Error(ST_ERR_INVALID, "Missing tensor: " + name);
+    const st_tensor* t = it->second;
+    std::vector<int> actual(t->shape, t->shape + std::max(0, std::min(2, t->rank)));
+    if (t->rank != (int)shape.size() || actual != shape) throw Error(ST_ERR_INVALID, "Shape mismatch: " + name);
+    return t;
+  };
+  const int wb = prec_ == kFp32 ? 4 : 2;
+  std::vector<unsigned char> host;
+  auto align = [&]() { host.resize((host.size() + 255) / 256 * 256, 0); };
+  auto put = [&](float v) {
+    if (prec_ == kFp32) {
+      unsigned char b[4];
+      std::memcpy(b, &v, 4);
+      host.insert(host.end(), b, b + 4);
+    } else {
+      uint16_t h;
+      if (prec_ == kMixed) {
+        h = host_half_bits(v);
+        if (host_half_to_float(h) != v && !std::isnan(v))
+          throw Error(ST_ERR_INVALID, "Mixed checkpoint tensor value is not FP16-representable");
+      } else {
+        h = host_bf16_bits(v);
+      }
+      host.push_back((unsigned char)(h & 0xff));
+      host.push_back((unsigned char)(h >> 8));
+    }
+  };
+  auto put_rows = [&](const float* data, int rows, int cols, int cols_p) {
+    for (int r = 0; r < rows; r++) {
+      for (int k = 0; k < cols; k++) put(data[(size_t)r * cols + k]);
+      for (int k = cols; k < cols_p; k++) put(0.f);
+    }
+  };
+  auto put_vector = [&](const float* data, int n) {
+    for (int i = 0; i < n; i++) put(data[i]);
+  };
+  StepArgs& a = args_;
+  const int d = c_.width, f = c_.ffn;
+  align();
+  a.w_input = (uint32_t)host.size();
+  put_rows(get("input", {d, c_.features})->data, d, c_.features, a.features_p);
+  for (int l = 0; l < c_.layers; l++) {
+    std::string p = "layers." + std::to_string(l) + ".";
+    LayerWeights& lw = a.layer[l];
+    align();
+    lw.norm1 = (uint32_t)host.size();
+    put_vector(get(p + "norm1", {d})->data, d);
+    align();
+    lw.norm2 = (uint32_t)host.size();
+    put_vector(get(p + "norm2", {d})->data, d);
+    align();
+    lw.qkv = (uint32_t)host.size();
+    put_rows(get(p + "q", {d, d})->data, d, d, a.width_p);
+    put_rows(get(p + "k", {d, d})->data, d, d, a.width_p);
+    put_rows(get(p + "v", {d, d})->data, d, d, a.width_p);
+    align();
+    lw.out = (uint32_t)host.size();
+    put_rows(get(p + "out", {d, d})->data, d, d, a.width_p);
+    align();
+    lw.gateup = (uint32_t)host.size();
+    const float* gate = get(p + "gate", {f, d})->data;
+    const float* up = get(p + "up", {f, d})->data;
+    for (int r = 0; r < f; r++) {
+      put_rows(gate + (size_t)r * d, 1, d, a.width_p);
+      put_rows(up + (size_t)r * d, 1, d, a.width_p);
+    }
+    align();
+    lw.down = (uint32_t)host.size();
+    put_rows(get(p + "down", {d, f})->data, d, f, a.ffn_p);
+  }
+  align();
+  a.w_final_norm = (uint32_t)host.size();
+  put_vector(get("final_norm", {d})->data, d);
+  align();
+  a.w_score = (uint32_t)host.size();
+  put_rows(get("score", {1, d})->data, 1, d, a.width_p);
+  align();
+  host.resize(host.size() + 256, 0);
+  if (host.size() > (size_t)std::numeric_limits<int>::max())
+    throw Error(ST_ERR_INVALID, "Weight arena exceeds 2 GiB");
+  (void)wb;
+  weights_.alloc(host.size());
+  HIP_CHECK(hipMemcpy(weights_.ptr, host.data(), host.size(), hipMemcpyHostToDevice));
+  a.weights = reinterpret_cast<const char*>(weights_.ptr);
+  a.weight_bytes = (uint32_t)host.size();
+}
+
+template <int P>
+void Runtime::launch_phases_t() {
+  const int nph = 5 * c_.layers + 2;
+  for (int ph = 0; ph < nph; ph++) {
+    int grid = ph == nph - 1 ? 1 : grid_;
+    hipLaunchKernelGGL(phase_kernel<P>, dim3(grid), dim3(kThreads), 0, stream_, dargs_, ph);
+  }
+  HIP_CHECK(hipGetLastError());
+}
+
+void Runtime::launch_phases() {
+  switch (prec_) {
+    case kFp32: launch_phases_t<kFp32>(); break;
+    case kMixed: launch_phases_t<kMixed>(); break;
+    default: launch_phases_t<kBf16w>(); break;
+  }
+}
+
+template <int P>
+void Runtime::launch_fused_t() {
+  if (grid_ == 1) {
+    hipLaunchKernelGGL(fused_kernel<P>, dim3(1), dim3(kThreads), 0, stream_, dargs_);
+  } else {
+    void* params[] = {&dargs_};
+    HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<void*>(fused_kernel<P>), dim3(grid_),
+                                         dim3(kThreads), params, 0, stream_));
+  }
+  HIP_CHECK(hipGetLastError());
+}
+
+void Runtime::launch_fused() {
+  switch (prec_) {
+    case kFp32: launch_fused_t<kFp32>(); break;
+    case kMixed: launch_fused_t<kMixed>(); break;
+    default: launch_fused_t<kBf16w>(); break;
+  }
+}
+
+void Runtime::launch_step() {
+  if (opt_.backend == ST_BACKEND_GRAPH) HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
+  else if (opt_.backend == ST_BACKEND_FUSED) launch_fused();
+  else launch_phases();
+}
+
+void Runtime::check_device_error() {
+  unsigned err = 0;
+  HIP_CHECK(hipMemcpy(&err, args_.error, 4, hipMemcpyDeviceToHost));
+  if (err) throw Error(ST_ERR_NUMERIC, "Device watchdog tripped (error bits " + std::to_string(err) + ")");
+}
+
+float Runtime::step(const float* input) {
+  if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
+  if (!input) throw Error(ST_ERR_INVALID, "Null input");
+  std::memcpy(host_in_.ptr, input, (size_t)c_.features * 4);
+  HIP_CHECK(hipMemcpyAsync(args_.scratch + args_.s_input, host_in_.ptr, (size_t)args_.features_p * 4,
+                           hipMemcpyHostToDevice, stream_));
+  launch_step();
+  HIP_CHECK(hipMemcpyAsync(host_out_.ptr, args_.scratch + args_.s_score, 8, hipMemcpyDeviceToHost, stream_));
+  sync();
+  const float* out = reinterpret_cast<const float*>(host_out_.ptr);
+  unsigned err;
+  std::memcpy(&err, out + 1, 4);
+  if (err) throw Error(ST_ERR_NUMERIC, "Device watchdog tripped (error bits " + std::to_string(err) + ")");
+  return out[0];
+}
+
+void Runtime::reset() {
+  if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
+  hipLaunchKernelGGL(reset_kernel, dim3(std::max(1, std::min(cus_, 1024))), dim3(256), 0, stream_, dargs_);
+  HIP_CHECK(hipGetLastError());
+  sync();
+}
+
+void Runtime::stop() {
+  if (running_) {
+    sync();
+    running_ = false;
+  }
+}
+
+void Runtime::snapshot(uint64_t* position, float* keys, float* values, float* hidden) {
+  sync();
+  if (position) HIP_CHECK(hipMemcpy(position, args_.position, 8, hipMemcpyDeviceToHost));
+  const size_t n = (size_t)c_.layers * c_.width * c_.window;
+  auto download = [&](const void* src, float* dst) {
+    if (!dst) return;
+    if (prec_ == kMixed) {
+      std::vector<uint16_t> h(n);
+      HIP_CHECK(hipMemcpy(h.data(), src, n * 2, hipMemcpyDeviceToHost));
+      for (size_t i = 0; i < n; i++) dst[i] = host_half_to_float(h[i]);
+    } else {
+      HIP_CHECK(hipMemcpy(dst, src, n * 4, hipMemcpyDeviceToHost));
+    }
+  };
+  download(args_.keys, keys);
+  download(args_.values, values);
+  if (hidden)
+    HIP_CHECK(hipMemcpy(hidden, args_.scratch + args_.s_hidden, (size_t)c_.layers * c_.width * 4,
+                        hipMemcpyDeviceToHost));
+}
+
+template <int P>
+void Runtime::launch_trace_t(const float* events, int count, unsigned long long* stamps) {
+  if (grid_ == 1) {
+    hipLaunchKernelGGL(trace_kernel<P>, dim3(1), dim3(kThreads), 0, stream_, dargs_, events, count, stamps);
+  } else {
+    void* params[] = {&dargs_, &events, &count, &stamps};
+    HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<void*>(trace_kernel<P>), dim3(grid_),
+                                         dim3(kThreads), params, 0, stream_));
+  }
+  HIP_CHECK(hipGetLastError());
+}
+
+double Runtime::device_trace(const float* inputs, size_t count, double* per_event) {
+  if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
+  if (!inputs || count == 0 || count > (size_t)std::numeric_limits<int>::max())
+    throw Error(ST_ERR_INVALID, "Invalid trace");
+  const int fp = args_.features_p;
+  std::vector<float> padded(count * (size_t)fp, 0.f);
+  for (size_t i = 0; i < count; i++)
+    std::memcpy(&padded[i * fp], inputs + i * c_.features, (size_t)c_.features * 4);
+  DeviceBuffer trace;
+  trace.alloc(padded.size() * 4);
+  HIP_CHECK(hipMemcpy(trace.ptr, padded.data(), padded.size() * 4, hipMemcpyHostToDevice));
+  reset();
+  std::vector<double> durations(count);
+  double mean = 0;
+  if (opt_.backend == ST_BACKEND_FUSED) {
+    DeviceBuffer stamps;
+    stamps.alloc((count + 1) * 8);
+    const float* ev = reinterpret_cast<const float*>(trace.ptr);
+    switch (prec_) {
+      case kFp32: launch_trace_t<kFp32>(ev, (int)count, (unsigned long long*)stamps.ptr); break;
+      case kMixed: launch_trace_t<kMixed>(ev, (int)count, (unsigned long long*)stamps.ptr); break;
+      default: launch_trace_t<kBf16w>(ev, (int)count, (unsigned long long*)stamps.ptr); break;
+    }
+    sync();
+    std::vector<unsigned long long> st(count + 1);
+    HIP_CHECK(hipMemcpy(st.data(), stamps.ptr, st.size() * 8, hipMemcpyDeviceToHost));
+    for (size_t i = 0; i < count; i++) durations[i] = (double)(st[i + 1] - st[i]) * 1000.0 / wall_khz_;
+    mean = (double)(st[count] - st[0]) * 1000.0 / wall_khz_ / count;
+  } else {
+    std::vector<hipEvent_t> ev(count + 1);
+    for (auto& e : ev) HIP_CHECK(hipEventCreate(&e));
+    HIP_CHECK(hipEventRecord(ev[0], stream_));
+    for (size_t i = 0; i < count; i++) {
+      HIP_CHECK(hipMemcpyAsync(args_.scratch + args_.s_input, reinterpret_cast<float*>(trace.ptr) + i * fp,
+                               (size_t)fp * 4, hipMemcpyDeviceToDevice, stream_));
+      launch_step();
+      HIP_CHECK(hipEventRecord(ev[i + 1], stream_));
+    }
+    sync();
+    for (size_t i = 0; i < count; i++) {
+      float ms = 0;
+      HIP_CHECK(hipEventElapsedTime(&ms, ev[i], ev[i + 1]));
+      durations[i] = ms * 1000.0;
+    }
+    float total = 0;
+    HIP_CHECK(hipEventElapsedTime(&total, ev[0], ev[count]));
+    mean = total * 1000.0 / count;
+    for (auto& e : ev) (void)hipEventDestroy(e);
+  }
+  check_device_error();
+  if (per_event) std::copy(durations.begin(), durations.end(), per_event);
+  return mean;
+}
+
+std::string Runtime::info() {
+  hipFuncAttributes fa{};
+  const void* fn = nullptr;
+  std::string name;
+  bool fused = opt_.backend == ST_BACKEND_FUSED;
+  switch (prec_) {
+    case kFp32: fn = fused ? (const void*)fused_kernel<kFp32> : (const void*)phase_kernel<kFp32>; break;
+    case kMixed: fn = fused ? (const void*)fused_kernel<kMixed> : (const void*)phase_kernel<kMixed>; break;
+    default: fn = fused ? (const void*)fused_kernel<kBf16w> : (const void*)phase_kernel<kBf16w>; break;
+  }
+  name = fused ? "fused_kernel" : "phase_kernel";
+  HIP_CHECK(hipFuncGetAttributes(&fa, fn));
+  static const char* backends[] = {"cuda(staged)", "graph", "cublas", "cublas-graph", "fused", "persistent"};
+  static const char* precs[] = {"fp32", "mixed", "bf16w"};
+  std::ostringstream o;
+  o << "{\"environment\": " << probe_ << ", \"backend\": \"" << backends[opt_.backend]
+    << "\", \"precision\": \"" << precs[prec_] << "\", \"blocks\": " << grid_
+    << ", \"threads\": " << kThreads << ", \"legal_cooperative_blocks\": " << legal_blocks_
+    << ", \"resource_kernel\": \"" << name << "\", \"registers_per_thread\": " << fa.numRegs
+    << ", \"local_bytes\": " << fa.localSizeBytes << ", \"shared_bytes\": " << fa.sharedSizeBytes
+    << ", \"phases_per_step\": " << 5 * c_.layers + 2 << ", \"prefetch_slabs\": " << kPF
+    << ", \"attention_chunk\": " << args_.chunk << ", \"weight_arena_bytes\": " << args_.weight_bytes
+    << ", \"matvec_implementation\": \"wave64 16-byte buffer loads, register ring, butterfly reduction\""
+    << ", \"attention_implementation\": \"LDS-staged window chunks, last-arriver head combine\""
+    << ", \"transport\": \"pinned-copy-stream-sync\""
+    << ", \"weights_and_kv_storage\": \""
+    << (prec_ == kMixed ? "FP16/FP16" : prec_ == kBf16w ? "BF16/FP32" : "FP32/FP32") << "\"}";
+  return o.str();
+}
+
+}  // namespace stamd
+
+// ---------------------------------------------------------------------------------------------
+// C ABI
+
+struct st_runtime {
+  std::unique_ptr<stamd::Runtime> impl;
+};
+
+template <class F>
+static int guarded(F&& f) {
+  try {
+    f();
+    stamd::g_last_error.clear();
+    return ST_OK;
+  } catch (const stamd::Error& e) {
+    stamd::g_last_error = e.what();
+    return e.code;
+  } catch (const std::exception& e) {
+    stamd::g_last_error = e.what();
+    return ST_ERR_DEVICE;
+  } catch (...) {
+    stamd::g_last_error = "unknown error";
+    return ST_ERR_DEVICE;
+  }
+}
+
+static int write_string(const std::string& s, char* buffer, size_t cap, size_t* needed) {
+  if (needed) *needed = s.size() + 1;
+  if (buffer && cap) {
+    size_t n = std::min(cap - 1, s.size());
+    std::memcpy(buffer, s.data(), n);
+    buffer[n] = 0;
+  }
+  return ST_OK;
+}
+
+extern "C" {
+
+void st_options_default(st_options* o) {
+  if (!o) return;
+  std::memset(o, 0, sizeof(*o));
+  o->backend = ST_BACKEND_GRAPH;
+  o->blocks = 1;
+  o->idle_seconds = 30;
+}
+
+int st_runtime_create(const st_config* config, int32_t mixed, const st_tensor* tensors, size_t count,
+                      const st_options* options, st_runtime** out) {
+  return guarded([&] {
+    if (!config || !tensors || !out) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    *out = nullptr;
+    st_options o;
+    if (options) o = *options;
+    else st_options_default(&o);
+    auto r = std::make_unique<st_runtime>();
+    r->impl = std::make_unique<stamd::Runtime>(*config, mixed != 0, tensors, count, o);
+    *out = r.release();
+  });
+}
+
+void st_runtime_destroy(st_runtime* r) {
+  if (!r) return;
+  try {
+    r->impl.reset();
+  } catch (...) {
+  }
+  delete r;
+}
+
+int st_runtime_step(st_runtime* r, const float* input, float* score) {
+  return guarded([&] {
+    if (!r || !score) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    *score = r->impl->step(input);
+  });
+}
+
+int st_runtime_reset(st_runtime* r) {
+  return guarded([&] {
+    if (!r) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    r->impl->reset();
+  });
+}
+
+int st_runtime_stop(st_runtime* r) {
+  return guarded([&] {
+    if (!r) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    r->impl->stop();
+  });
+}
+
+int st_runtime_snapshot(st_runtime* r, uint64_t* position, float* keys, float* values, float* hidden) {
+  return guarded([&] {
+    if (!r) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    r->impl->snapshot(position, keys, values, hidden);
+  });
+}
+
+int st_runtime_device_trace(st_runtime* r, const float* inputs, size_t count, double* us_per_event,
+                            double* per_event_us) {
+  return guarded([&] {
+    if (!r || !us_per_event) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    *us_per_event = r->impl->device_trace(inputs, count, per_event_us);
+  });
+}
+
+int st_runtime_info_json(st_runtime* r, char* buffer, size_t cap, size_t* needed) {
+  return guarded([&] {
+    if (!r) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    write_string(r->impl->info(), buffer, cap, needed);
+  });
+}
+
+int st_probe_json(char* buffer, size_t cap, size_t* needed) {
+  return guarded([&] { write_string(stamd::probe_json(), buffer, cap, needed); });
+}
+
+const char* st_last_error(void) { return stamd::g_last_error.c_str(); }
+
+}  // extern "C"

@@ -1,0 +1,228 @@
+"""ctypes binding of libstamd.so, mirroring Stream::Runtime (include/Runtime.hpp:7-46).
+
+Same names and meaning as the reference interface: ``Runtime(model, options)``, ``step``,
+``reset``, ``stop``, ``snapshot``, ``info``, ``device_trace``, plus ``probe()``. Failures
+raise ``RuntimeError`` with the library's message, as the reference throws
+``std::runtime_error``. There is no fallback: if the HIP library is missing or cannot be
+loaded, constructing a runtime raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import json
+import os
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+from .model import Checkpoint, ModelConfig
+
+PACKAGE_DIR = Path(__file__).resolve().parent.parent
+LIBRARY_PATH = PACKAGE_DIR / 'lib' / 'libstamd.so'
+
+
+class Backend(enum.IntEnum):
+    """Stream::Backend (include/Runtime.hpp:7)."""
+    CUDA = 0          # staged HIP phase kernels
+    GRAPH = 1         # staged sequence captured in a hipGraph
+    CUBLAS = 2        # not provided
+    CUBLAS_GRAPH = 3  # not provided
+    FUSED = 4         # one cooperative launch per step
+    PERSISTENT = 5    # resident kernel + host mailbox
+
+
+class WeightStorage(enum.IntEnum):
+    AS_MODEL = 0
+    BF16 = 1
+
+
+@dataclass
+class RuntimeOptions:
+    """Stream::RuntimeOptions (include/Runtime.hpp:8-19) plus weight storage.
+    blocks = workgroups of 512 threads; 0 = one per compute unit."""
+    backend: Backend = Backend.GRAPH
+    blocks: int = 1
+    backoff: bool = False
+    mapped: bool = False
+    vector_matvec: bool = False
+    fused_attention: bool = False
+    max_events: int = 0
+    initial_sequence: int = 0
+    idle_seconds: float = 30.0
+    weight_dtype: WeightStorage = WeightStorage.AS_MODEL
+
+
+class _Config(ctypes.Structure):
+    _fields_ = [('layers', ctypes.c_int32), ('width', ctypes.c_int32), ('heads', ctypes.c_int32),
+                ('ffn', ctypes.c_int32), ('window', ctypes.c_int32), ('features', ctypes.c_int32),
+                ('epsilon', ctypes.c_float)]
+
+
+class _Options(ctypes.Structure):
+    _fields_ = [('backend', ctypes.c_int32), ('blocks', ctypes.c_int32), ('backoff', ctypes.c_int32),
+                ('mapped', ctypes.c_int32), ('vector_matvec', ctypes.c_int32),
+                ('fused_attention', ctypes.c_int32), ('max_events', ctypes.c_uint64),
+                ('initial_sequence', ctypes.c_uint64), ('idle_seconds', ctypes.c_double),
+                ('weight_dtype', ctypes.c_int32), ('reserved', ctypes.c_int32)]
+
+
+class _Tensor(ctypes.Structure):
+    _fields_ = [('name', ctypes.c_char_p), ('rank', ctypes.c_int32), ('shape', ctypes.c_int32 * 2),
+                ('data', ctypes.POINTER(ctypes.c_float))]
+
+
+_lib = None
+
+
+def library(path: os.PathLike | None = None) -> ctypes.CDLL:
+    """Load libstamd.so (once). Raises RuntimeError if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = Path(path or os.environ.get('STAMD_LIBRARY', LIBRARY_PATH))
+    if not path.exists():
+        raise RuntimeError(f'HIP library not built: {path} (run __graft_entry__.build())')
+    lib = ctypes.CDLL(str(path))
+    P, F, D = ctypes.c_void_p, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_double)
+    lib.st_options_default.argtypes = [ctypes.POINTER(_Options)]
+    lib.st_options_default.restype = None
+    lib.st_runtime_create.argtypes = [ctypes.POINTER(_Config), ctypes.c_int32, ctypes.POINTER(_Tensor),
+                                      ctypes.c_size_t, ctypes.POINTER(_Options), ctypes.POINTER(P)]
+    lib.st_runtime_destroy.argtypes = [P]
+    lib.st_runtime_destroy.restype = None
+    lib.st_runtime_step.argtypes = [P, F, F]
+    lib.st_runtime_reset.argtypes = [P]
+    lib.st_runtime_stop.argtypes = [P]
+    lib.st_runtime_snapshot.argtypes = [P, ctypes.POINTER(ctypes.c_uint64), F, F, F]
+    lib.st_runtime_device_trace.argtypes = [P, F, ctypes.c_size_t, D, D]
+    lib.st_runtime_info_json.argtypes = [P, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+    lib.st_probe_json.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+    lib.st_last_error.argtypes = []
+    lib.st_last_error.restype = ctypes.c_char_p
+    for name in ('st_runtime_create', 'st_runtime_step', 'st_runtime_reset', 'st_runtime_stop',
+                 'st_runtime_snapshot', 'st_runtime_device_trace', 'st_runtime_info_json', 'st_probe_json'):
+        getattr(lib, name).restype = ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise RuntimeError(library().st_last_error().decode() or f'libstamd error {status}')
+
+
+def _fptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def _json(fn, *args) -> dict:
+    needed = ctypes.c_size_t(0)
+    _check(fn(*args, None, 0, ctypes.byref(needed)))
+    buf = ctypes.create_string_buffer(needed.value)
+    _check(fn(*args, buf, needed.value, ctypes.byref(needed)))
+    return json.loads(buf.value.decode())
+
+
+def probe() -> dict:
+    """Stream::probe() (src/cuda/Runtime.cu:134-161)."""
+    return _json(library().st_probe_json)
+
+
+class Runtime:
+    """Stream::Runtime over the C ABI. ``model`` is a Checkpoint, or a (config, tensors,
+    mixed) triple. Not thread-safe; one outstanding command (docs/transport.md:14)."""
+
+    def __init__(self, model, options: RuntimeOptions | None = None):
+        if isinstance(model, Checkpoint):
+            config, tensors, mixed = model.config, model.tensors, model.mixed
+        else:
+            config, tensors, mixed = model
+        self.config: ModelConfig = config
+        self.mixed = bool(mixed)
+        self.options = options or RuntimeOptions()
+        lib = library()
+        cfg = _Config(config.layers, config.width, config.heads, config.ffn, config.window,
+                      config.features, config.epsilon)
+        keep, items = [], []
+        # Pass every named tensor; the library validates names, shapes and the config.
+        for name in sorted(tensors):
+            a = np.ascontiguousarray(tensors[name], dtype=np.float32)
+            keep.append(a)
+            t = _Tensor()
+            t.name = name.encode()
+            t.rank = a.ndim
+            t.shape[0] = a.shape[0]
+            t.shape[1] = a.shape[1] if a.ndim > 1 else 0
+            t.data = _fptr(a)
+            items.append(t)
+        array = (_Tensor * len(items))(*items)
+        o = self.options
+        opts = _Options(int(o.backend), int(o.blocks), int(o.backoff), int(o.mapped), int(o.vector_matvec),
+                        int(o.fused_attention), int(o.max_events), int(o.initial_sequence),
+                        float(o.idle_seconds), int(o.weight_dtype), 0)
+        handle = ctypes.c_void_p()
+        _check(lib.st_runtime_create(ctypes.byref(cfg), int(self.mixed), array, len(items), ctypes.byref(opts),
+                                     ctypes.byref(handle)))
+        self._h = handle
+        self._score = np.zeros(1, dtype=np.float32)
+
+    def close(self) -> None:
+        """Stop the worker and free device resources (~Runtime)."""
+        if getattr(self, '_h', None):
+            library().st_runtime_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _handle(self):
+        if not self._h:
+            raise RuntimeError('Runtime is closed')
+        return self._h
+
+    def step(self, event) -> float:
+        x = np.ascontiguousarray(event, dtype=np.float32)
+        if x.size != self.config.features:
+            raise ValueError('event must hold `features` floats')
+        _check(library().st_runtime_step(self._handle(), _fptr(x), _fptr(self._score)))
+        return float(self._score[0])
+
+    def reset(self) -> None:
+        _check(library().st_runtime_reset(self._handle()))
+
+    def stop(self) -> None:
+        _check(library().st_runtime_stop(self._handle()))
+
+    def snapshot(self):
+        """(position, keys[L,H,W,dh], values[L,H,W,dh], hidden[L,width]) as FP32."""
+        c = self.config
+        keys = np.empty((c.layers, c.heads, c.window, c.dim), dtype=np.float32)
+        values = np.empty_like(keys)
+        hidden = np.empty((c.layers, c.width), dtype=np.float32)
+        pos = ctypes.c_uint64(0)
+        _check(library().st_runtime_snapshot(self._handle(), ctypes.byref(pos), _fptr(keys), _fptr(values),
+                                             _fptr(hidden)))
+        return int(pos.value), keys, values, hidden
+
+    def device_trace(self, inputs):
+        """Runtime::deviceTrace: reset, run a preloaded trace; (mean us, per-event us)."""
+        x = np.ascontiguousarray(inputs, dtype=np.float32).reshape(-1, self.config.features)
+        per = np.empty(x.shape[0], dtype=np.float64)
+        mean = ctypes.c_double(0)
+        _check(library().st_runtime_device_trace(self._handle(), _fptr(x), x.shape[0], ctypes.byref(mean),
+                                                 per.ctypes.data_as(ctypes.POINTER(ctypes.c_double))))
+        return float(mean.value), per
+
+    def info(self) -> dict:
+        return _json(library().st_runtime_info_json, self._handle())

@@ -1,0 +1,206 @@
+"""GPU parity of libstamd.so against the reference's golden vectors and the CPU oracle.
+
+Every test calls the HIP path through the C ABI (streamtx.runtime). Bars:
+  - reference fixtures: the reference's tolerances (FP32 1e-5 + 1e-4|r|, mixed v3 policy);
+  - CPU oracle (FP64-accumulating referee): FP32 within 1e-6 + 1e-5|r| per step, for the
+    score and the complete carried state;
+  - backends (staged, graph, fused, grid sizes): bit-identical to each other.
+"""
+import numpy as np
+import pytest
+
+from oracle.pyoracle import Oracle
+from streamtx import (Backend, ModelConfig, Runtime, RuntimeOptions, WeightStorage, numerical, round_bf16,
+                      synthetic_checkpoint)
+
+pytestmark = pytest.mark.gpu
+
+STRICT = dict(atol=1e-6, rtol=1e-5)
+BACKENDS = [(Backend.CUDA, 0), (Backend.GRAPH, 0), (Backend.FUSED, 1), (Backend.FUSED, 4), (Backend.FUSED, 0)]
+
+
+def runtime(model, backend, blocks, **kw):
+    print(f'[case] backend={Backend(backend).name} blocks={blocks} {kw}', flush=True)
+    return Runtime(model, RuntimeOptions(backend=backend, blocks=blocks, **kw))
+
+
+@pytest.mark.parametrize('backend,blocks', BACKENDS)
+def test_fp32_fixture_every_event(golden, backend, blocks):
+    g = golden('small-fp32')
+    oracle = Oracle(g.config, g.checkpoint.tensors, accumulate='double')
+    with runtime(g.checkpoint, backend, blocks) as rt:
+        for i, score, keys, values, hidden in g.expected_state():
+            if i in g.resets:
+                rt.reset()
+                oracle.reset()
+            got = rt.step(g.trace[i])
+            ref = oracle.step(g.trace[i])
+            pos, k, v, h = rt.snapshot()
+            _, ok, ov, oh = oracle.snapshot()
+            assert pos == oracle.position
+            assert numerical.fp32_failures([got], [score]) == 0, (i, got, score)
+            assert numerical.fp32_strict_failures([got], [ref], **STRICT) == 0, (i, got, ref)
+            for a, r, o in ((k, keys, ok), (v, values, ov), (h, hidden, oh)):
+                assert numerical.fp32_failures(a, r) == 0, i
+                assert numerical.fp32_strict_failures(a, o, **STRICT) == 0, (i, float(np.abs(a - o).max()))
+
+
+@pytest.mark.parametrize('backend,blocks', [(Backend.CUDA, 0), (Backend.GRAPH, 0), (Backend.FUSED, 0)])
+def test_mixed_fixture_policy_v3(golden, backend, blocks):
+    g = golden('small-mixed')
+    scores, refs = [], []
+    with runtime(g.checkpoint, backend, blocks) as rt:
+        for i, score, keys, values, hidden in g.expected_state():
+            if i in g.resets:
+                rt.reset()
+            scores.append(rt.step(g.trace[i]))
+            refs.append(score)
+            _, k, v, h = rt.snapshot()
+            res = numerical.mixed_state_passes(k, v, h, keys, values, hidden)
+            assert res['passed'], (i, res['failures'][:2])
+            for a in (k, v, h):
+                assert np.array_equal(a, a.astype(np.float16).astype(np.float32))
+    res = numerical.score_errors(scores, refs, g.config.layers)
+    assert res['passed'], res
+
+
+def _stream(config, seed, count):
+    return np.random.default_rng(seed).standard_normal((count, config.features)).astype(np.float32)
+
+
+SHAPES = {
+    # BASELINE configurations with features = d_model (SwiGLU, RoPE, norm weights 1)
+    'small': ModelConfig(4, 256, 4, 1024, 64, 256),
+    'main': ModelConfig(8, 512, 8, 2048, 128, 512),
+    'large': ModelConfig(12, 1024, 16, 4096, 512, 1024),
+    # reference fixture shapes with head dim 32 (configs/main.json, configs/large.json)
+    'ref-main': ModelConfig(2, 128, 4, 256, 256, 32),
+    'ref-large': ModelConfig(4, 256, 8, 512, 512, 32),
+}
+
+
+@pytest.mark.parametrize('name,steps,reset_at', [('small', 160, 137), ('main', 40, None), ('large', 12, None),
+                                                 ('ref-main', 300, 261), ('ref-large', 64, None)])
+def test_fused_matches_oracle_at_shape(name, steps, reset_at):
+    c = SHAPES[name]
+    w = synthetic_checkpoint(c, seed=1)
+    events = _stream(c, 1, steps)
+    oracle = Oracle(c, w, accumulate='double', threads=8)
+    with runtime((c, w, False), Backend.FUSED, 0) as rt:
+        for i, e in enumerate(events):
+            if i == reset_at:
+                rt.reset()
+                oracle.reset()
+            got, ref = rt.step(e), oracle.step(e)
+            assert numerical.fp32_strict_failures([got], [ref], **STRICT) == 0, (i, got, ref)
+        pos, k, v, h = rt.snapshot()
+        opos, ok, ov, oh = oracle.snapshot()
+        assert pos == opos
+        for a, o in ((k, ok), (v, ov), (h, oh)):
+            assert numerical.fp32_strict_failures(a, o, **STRICT) == 0, float(np.abs(a - o).max())
+
+
+@pytest.mark.parametrize('name,steps', [('small', 150), ('main', 140), ('ref-main', 64)])
+def test_backends_are_bit_identical(name, steps):
+    c = SHAPES[name]
+    w = synthetic_checkpoint(c, seed=2)
+    events = _stream(c, 2, steps)
+    results = []
+    for backend, blocks in BACKENDS:
+        with runtime((c, w, False), backend, blocks) as rt:
+            scores = np.array([rt.step(e) for e in events], dtype=np.float32)
+            results.append((scores, rt.snapshot()))
+    base_scores, base_state = results[0]
+    for scores, state in results[1:]:
+        np.testing.assert_array_equal(scores, base_scores)
+        assert state[0] == base_state[0]
+        for a, b in zip(state[1:], base_state[1:]):
+            np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize('mixed', [False, True])
+def test_zero_input_scores_zero(mixed):
+    c = ModelConfig(2, 256, 4, 512, 16, 256)
+    w = synthetic_checkpoint(c, seed=4, mixed=mixed)
+    zero = np.zeros(c.features, dtype=np.float32)
+    with runtime((c, w, mixed), Backend.FUSED, 0) as rt:
+        for i in range(3 * c.window + 9):
+            if i in (1, c.window, 2 * c.window + 3):
+                rt.reset()
+                rt.reset()
+                assert rt.snapshot()[0] == 0
+            assert rt.step(zero) == 0.0
+
+
+@pytest.mark.parametrize('backend', [Backend.FUSED, Backend.GRAPH])
+def test_device_trace_equals_stepping(backend):
+    c = SHAPES['main']
+    w = synthetic_checkpoint(c, seed=5)
+    events = _stream(c, 5, 70)
+    with runtime((c, w, False), backend, 0) as rt:
+        for e in events:
+            rt.step(e)
+        stepped = rt.snapshot()
+        mean, per = rt.device_trace(events)
+        traced = rt.snapshot()
+    assert mean > 0 and per.shape == (len(events),) and np.all(per > 0)
+    assert traced[0] == stepped[0]
+    for a, b in zip(traced[1:], stepped[1:]):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_bf16_weights_equal_fp32_model_on_rounded_weights():
+    c = SHAPES['main']
+    w = synthetic_checkpoint(c, seed=6)
+    rounded = {k: round_bf16(v) for k, v in w.items()}
+    oracle = Oracle(c, rounded, accumulate='double', threads=8)
+    events = _stream(c, 6, 40)
+    with runtime((c, w, False), Backend.FUSED, 0, weight_dtype=WeightStorage.BF16) as rt:
+        for e in events:
+            got, ref = rt.step(e), oracle.step(e)
+            assert numerical.fp32_strict_failures([got], [ref], **STRICT) == 0, (got, ref)
+        _, k, v, h = rt.snapshot()
+    _, ok, ov, oh = oracle.snapshot()
+    for a, o in ((k, ok), (v, ov), (h, oh)):
+        assert numerical.fp32_strict_failures(a, o, **STRICT) == 0
+
+
+def test_mixed_baseline_shape_policy_v3():
+    c = SHAPES['main']
+    w = synthetic_checkpoint(c, seed=7, mixed=True)
+    events = _stream(c, 7, 40)
+    oracle = Oracle(c, w, mixed=True, threads=8)
+    scores, refs = [], []
+    with runtime((c, w, True), Backend.FUSED, 0) as rt:
+        for e in events:
+            scores.append(rt.step(e))
+            refs.append(oracle.step(e))
+        _, k, v, h = rt.snapshot()
+    _, ok, ov, oh = oracle.snapshot()
+    assert numerical.mixed_state_passes(k, v, h, ok, ov, oh)['passed']
+    assert numerical.score_errors(scores, refs, c.layers)['passed']
+
+
+def test_cooperative_grid_limit_and_info():
+    c = SHAPES['small']
+    w = synthetic_checkpoint(c, seed=8)
+    with runtime((c, w, False), Backend.FUSED, 0) as rt:
+        info = rt.info()
+    assert info['environment']['arch'].startswith('gfx950')
+    assert info['blocks'] == info['environment']['compute_units']
+    assert info['legal_cooperative_blocks'] >= info['blocks']
+    with pytest.raises(RuntimeError, match='occupancy limit'):
+        Runtime((c, w, False), RuntimeOptions(backend=Backend.FUSED, blocks=info['legal_cooperative_blocks'] + 1))
+
+
+def test_stopped_runtime_rejects_commands():
+    c = SHAPES['small']
+    w = synthetic_checkpoint(c, seed=9)
+    with runtime((c, w, False), Backend.GRAPH, 0) as rt:
+        rt.step(np.ones(c.features, np.float32))
+        rt.stop()
+        rt.stop()
+        with pytest.raises(RuntimeError, match='stopped'):
+            rt.step(np.ones(c.features, np.float32))
+        with pytest.raises(RuntimeError, match='stopped'):
+            rt.reset()
