@@ -1,0 +1,183 @@
+"""Benchmark of the streaming-step hot path on one MI355X.
+
+Headline workload: Large FP32, W=512, one stream (d_model 1024, 12 layers, 16 heads x 64,
+SwiGLU FFN 4096, RMSNorm eps 1e-5, features = d_model), synthetic weights ~ N(0, 0.02^2)
+and inputs ~ N(0, 1) from seed 3. A "step" is one event through the whole model: input
+projection, 12 layers, final norm and score, with the K/V rings carried on the GPU.
+
+Timing: the window is first filled (W-1 events) and warmed (--warmup events), untimed;
+then exactly --steps full-window steps run through the fused backend, one cooperative
+launch per step, with a HIP event recorded on the runtime's stream after each launch
+(st_runtime_device_run). `value` is the p50 of those per-step device durations (inputs
+already resident in HBM). The library synchronizes its stream before and after the timed
+launches. One JSON line is printed.
+
+Usage: python bench.py [--gpus 1] [--steps 1024] [--warmup 64] [--config large|main|small]
+                       [--precision fp32|bf16w|mixed] [--no-cpu-baseline] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT, ROOT / 'streaming-transformer_amd'):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+from streamtx import Backend, ModelConfig, Runtime, RuntimeOptions, WeightStorage, synthetic_checkpoint  # noqa: E402
+
+CONFIGS = {
+    'small': (ModelConfig(4, 256, 4, 1024, 64, 256), 0),
+    'main': (ModelConfig(8, 512, 8, 2048, 128, 512), 1),
+    'large': (ModelConfig(12, 1024, 16, 4096, 512, 1024), 3),
+}
+HBM_PEAK_GBS = 8000.0
+METRIC = 'p50 µs per streaming step + matvec achieved HBM GB/s, Main/Large fp32'
+
+
+def weight_bytes_per_step(c: ModelConfig, wb: int) -> int:
+    """All matvec weights, norm weights and the score row read once per step."""
+    d, f, L = c.width, c.ffn, c.layers
+    return wb * (c.features * d + L * (4 * d * d + 3 * d * f + 2 * d) + 2 * d)
+
+
+def kv_bytes_per_step(c: ModelConfig, kvb: int, valid: int) -> int:
+    """K and V rows read over the valid window plus the new row written, every layer."""
+    return 2 * c.layers * c.width * valid * kvb + 2 * c.layers * c.width * kvb
+
+
+def nearest_rank(values, q):
+    v = np.sort(np.asarray(values))
+    return float(v[max(0, int(math.ceil(q * len(v))) - 1)])
+
+
+def cpu_baseline(c: ModelConfig, weights, mixed, events, fill: int, sample: int):
+    """The C oracle (a restatement of the reference CPU step) timed on this host:
+    single thread (the reference default), on `sample` full-window steps."""
+    from oracle.pyoracle import Oracle
+    threads_all = min(16, os.cpu_count() or 1)
+    oracle = Oracle(c, weights, mixed=mixed, threads=threads_all)
+    for e in events[:fill]:
+        oracle.step(e)
+    out = {}
+    for threads in (1, threads_all):
+        oracle_threads = threads
+        from oracle import pyoracle
+        pyoracle.library().so_set_threads(oracle._h, oracle_threads)
+        times = []
+        for e in events[fill:fill + sample]:
+            t0 = time.perf_counter()
+            oracle.step(e)
+            times.append((time.perf_counter() - t0) * 1e6)
+        out[threads] = times
+    return out, threads_all
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=1024)
+    ap.add_argument('--warmup', type=int, default=64)
+    ap.add_argument('--config', choices=sorted(CONFIGS), default='large')
+    ap.add_argument('--precision', choices=['fp32', 'bf16w', 'mixed'], default='fp32')
+    ap.add_argument('--backend', choices=['fused', 'graph', 'cuda'], default='fused')
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--quick', action='store_true', help='skip the secondary measurements')
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f'bench.py measures one GPU: the streaming step is a single ordered stream and this '
+              f'build does not shard it (requested --gpus {args.gpus}).', file=sys.stderr)
+        sys.exit(2)
+
+    c, seed = CONFIGS[args.config]
+    mixed = args.precision == 'mixed'
+    weights = synthetic_checkpoint(c, seed=seed, mixed=mixed)
+    fill = c.window - 1 + args.warmup
+    rng = np.random.default_rng([seed, 1])  # input stream distinct from the weight stream
+    events = rng.standard_normal((fill + args.steps, c.features), dtype=np.float32)
+    backend = {'fused': Backend.FUSED, 'graph': Backend.GRAPH, 'cuda': Backend.CUDA}[args.backend]
+    opts = RuntimeOptions(backend=backend, blocks=0,
+                          weight_dtype=WeightStorage.BF16 if args.precision == 'bf16w' else WeightStorage.AS_MODEL)
+    wb = 4 if args.precision == 'fp32' else 2
+    kvb = 2 if mixed else 4
+    bytes_step = weight_bytes_per_step(c, wb) + kv_bytes_per_step(c, kvb, c.window)
+
+    extra = {}
+    with Runtime((c, weights, mixed), opts) as rt:
+        info = rt.info()
+        rt.device_run(events[:fill], reset=True)                      # fill + warm up, untimed
+        t0 = time.perf_counter()
+        mean_us, per = rt.device_run(events[fill:fill + args.steps])  # exactly --steps launches
+        wall = time.perf_counter() - t0
+        p50 = nearest_rank(per, 0.5)
+        extra['p99_us'] = nearest_rank(per, 0.99)
+        extra['mean_us'] = mean_us
+        extra['wall_seconds_timed_call'] = wall
+        if not args.quick:
+            # Host-service latency through step(): pinned H2D input, launch, D2H score, sync.
+            host = []
+            for e in events[fill:fill + 256]:
+                s = time.perf_counter()
+                rt.step(e)
+                host.append((time.perf_counter() - s) * 1e6)
+            extra['host_service_p50_us'] = nearest_rank(host, 0.5)
+            extra['host_service_p99_us'] = nearest_rank(host, 0.99)
+            if backend == Backend.FUSED:
+                # Device loop inside one cooperative launch (the reference's deviceTrace).
+                n = c.window - 1 + 256
+                _, loop = rt.device_trace(events[:n])
+                extra['device_loop_p50_us'] = nearest_rank(loop[c.window - 1:], 0.5)
+
+    achieved = bytes_step / (mean_us * 1e-6) / 1e9
+    roofline = {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None,
+                'algorithmic_bytes_per_step': bytes_step,
+                'roofline_us_per_step': bytes_step / (HBM_PEAK_GBS * 1e9) * 1e6,
+                'kernel': 'fused_kernel' if backend == Backend.FUSED else 'phase_kernel sequence'}
+    traffic_file = ROOT / 'profiles' / f'traffic_{args.backend}_{args.config}_{args.precision}.json'
+    if traffic_file.exists():
+        t = json.loads(traffic_file.read_text())
+        roofline['traffic'] = t.get('hbm_bytes_per_launch')
+    roofline['frac_p50'] = round(bytes_step / (p50 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    extra['mall_resident'] = bytes_step < 256e6
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        sample = {'large': 12, 'main': 40, 'small': 200}[args.config]
+        cfill = {'large': c.window - 1, 'main': c.window - 1, 'small': c.window - 1}[args.config]
+        times, threads_all = cpu_baseline(c, weights if args.precision != 'bf16w' else
+                                          {k: __import__('streamtx').round_bf16(v) for k, v in weights.items()},
+                                          mixed, events, cfill, sample)
+        cpu = {'value': nearest_rank(times[1], 0.5), 'unit': 'us per step (p50)', 'cores': 1,
+               'kind': 'port',
+               'sample': f'{sample} full-window steps of the same {args.config} {args.precision} workload after a '
+                         f'{cfill}-event fill; C oracle restating src/cpu/Cpu.cpp:59-141, 1 thread',
+               'multithread_p50_us': nearest_rank(times[threads_all], 0.5), 'multithread_cores': threads_all}
+
+    line = {
+        'metric': METRIC, 'value': round(p50, 3), 'unit': 'us', 'n_gpus': 1, 'steps': args.steps,
+        'warmup': args.warmup, 'ms_per_step': round(mean_us / 1000.0, 6), 'higher_is_better': False,
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': {'fp32': 'fp32', 'bf16w': 'bf16 weights, fp32 compute',
+                                                          'mixed': 'fp16 storage, fp32 accumulate'}[args.precision],
+        'data': 'synthetic (weights N(0,0.02^2), inputs N(0,1))',
+        'config': {'workload': f'{args.config} {args.precision} single-stream step, W={c.window}',
+                   'd_model': c.width, 'layers': c.layers, 'heads': c.heads, 'head_dim': c.dim, 'ffn': c.ffn,
+                   'window': c.window, 'features': c.features, 'seed': seed, 'backend': args.backend,
+                   'blocks': info['blocks'], 'threads_per_block': info['threads']},
+        'roofline': roofline,
+        'cpu_baseline': cpu,
+        'extra': extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == '__main__':
+    main()

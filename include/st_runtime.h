@@ -122,6 +122,24 @@ int st_runtime_snapshot(st_runtime* runtime, uint64_t* position, float* keys, fl
 int st_runtime_device_trace(st_runtime* runtime, const float* inputs, size_t count,
                             double* us_per_event, double* per_event_us);
 
+/* Extension (no counterpart in the reference): per-launch device timing. Runs `count`
+ * events from a preloaded device copy, one step per launch (FUSED: one cooperative launch
+ * per event; CUDA/GRAPH: device-to-device staging copy plus the phase sequence), after a
+ * reset if `reset` is nonzero, otherwise continuing the current stream state. A HIP event
+ * is recorded on the runtime's stream after every step; per_event_us (may be NULL)
+ * receives the count event-to-event durations, *us_per_event their mean. */
+int st_runtime_device_run(st_runtime* runtime, const float* inputs, size_t count, int32_t reset,
+                          double* us_per_event, double* per_event_us);
+
+/* Extension (no counterpart in the reference): one FUSED step on `input` (advancing the
+ * stream like st_runtime_step) with wall-clock stamps from workgroup 0. For each of the
+ * 5*layers+2 phases writes four times in microseconds since the step started: phase start,
+ * first stream wave done with the phase, control wave starts staging the next phase's
+ * inputs, staging done (0 where not recorded); then the end of the step. Writes
+ * min(cap, 4*phases+1) values and the full count. */
+int st_runtime_phase_times(st_runtime* runtime, const float* input, double* us, size_t cap,
+                           size_t* count);
+
 /* Json Runtime::info() const - src/cuda/Runtime.cu:570-594, as a JSON string. Writes at
  * most cap bytes (NUL-terminated) and the full length to *needed. */
 int st_runtime_info_json(st_runtime* runtime, char* buffer, size_t cap, size_t* needed);

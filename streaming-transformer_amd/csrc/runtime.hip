@@ -1,8 +1,8 @@
 // Host runtime and C ABI of libstamd.so (see include/st_runtime.h).
 //
 // Owns the device state of one stream: a single weight arena laid out in phase order,
-// the K/V rings, an FP32 scratch arena, the device-held position and the grid-barrier
-// flags. Mirrors Stream::Runtime::Impl (src/cuda/Runtime.cu:167-653) behind a C ABI.
+// the K/V rings, an FP32 scratch arena, the epoch-tagged activation vectors, the
+// device-held position and epoch. Mirrors Stream::Runtime::Impl (src/cuda/Runtime.cu:167-653) behind a C ABI.
 #include "step_phases.hpp"
 #include "../../include/st_runtime.h"
 
@@ -21,6 +21,7 @@
 #include <stdexcept>
 #include <string>
 #include <thread>
+#include <type_traits>
 #include <vector>
 
 namespace stamd {
@@ -164,17 +165,35 @@ class Runtime {
   void stop();
   void snapshot(uint64_t* position, float* keys, float* values, float* hidden);
   double device_trace(const float* inputs, size_t count, double* per_event);
+  double device_run(const float* inputs, size_t count, bool reset_first, double* per_event);
+  size_t phase_times(const float* input, double* us, size_t cap);
   std::string info();
 
  private:
   void build_weights(const st_tensor* tensors, size_t count);
   void launch_step();
   void launch_phases();
-  void launch_fused();
-  template <int P> void launch_phases_t();
-  template <int P> void launch_fused_t();
-  template <int P> void launch_trace_t(const float* events, int count, unsigned long long* stamps);
-  template <int P> int legal_blocks_t();
+  void launch_fused(const float* event = nullptr);
+  template <int P, int A> void launch_phases_t();
+  template <int P, int A> void launch_fused_t(const float* event);
+  template <int P, int A> void launch_trace_t(const float* events, int count, unsigned long long* stamps);
+  template <int P, int A> int legal_blocks_t();
+  // Call f(precision, attention path) with both as integral constants.
+  template <class F> auto dispatch(F&& f) {
+    using I = std::integral_constant<int, 0>;
+    if (args_.attn_regs) {
+      switch (prec_) {
+        case kFp32: return f(std::integral_constant<int, kFp32>{}, std::integral_constant<int, 1>{});
+        case kMixed: return f(std::integral_constant<int, kMixed>{}, std::integral_constant<int, 1>{});
+        default: return f(std::integral_constant<int, kBf16w>{}, std::integral_constant<int, 1>{});
+      }
+    }
+    switch (prec_) {
+      case kFp32: return f(std::integral_constant<int, kFp32>{}, I{});
+      case kMixed: return f(std::integral_constant<int, kMixed>{}, I{});
+      default: return f(std::integral_constant<int, kBf16w>{}, I{});
+    }
+  }
   void check_device_error();
   void sync() { HIP_CHECK(hipStreamSynchronize(stream_)); }
 
@@ -186,7 +205,7 @@ class Runtime {
   hipStream_t stream_ = nullptr;
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;
-  DeviceBuffer weights_, keys_, values_, scratch_, counters_, position_, flags_, epoch_, rope_, args_dev_;
+  DeviceBuffer weights_, keys_, values_, scratch_, tagged_, counters_, position_, epoch_, rope_, args_dev_;
   PinnedBuffer host_in_, host_out_;
   StepArgs args_{};
   const StepArgs* dargs_ = nullptr;
@@ -242,6 +261,14 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   a.features_p = round_up(c_.features, slab);
   a.chunk = std::min(32, 2048 / dim_);
   if (a.chunk < 1) a.chunk = 1;
+  {
+    // Register attention: power-of-two head dim with E <= dim <= 64E (E = elements per
+    // 16-byte chunk) and a K/V block that is whole 16-byte chunks.
+    const int e = prec_ == kMixed ? 8 : 4;
+    const int kvb = prec_ == kMixed ? 2 : 4;
+    bool pow2 = (dim_ & (dim_ - 1)) == 0;
+    a.attn_regs = pow2 && dim_ >= e && dim_ <= 64 * e && (a.chunk * dim_ * kvb) % 16 == 0 ? 1 : 0;
+  }
 
   build_weights(tensors, count);
 
@@ -263,12 +290,6 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   };
   int vec = std::max({a.width_p, a.ffn_p, a.features_p});
   a.s_input = take(a.features_p);
-  a.s_x = take(a.width_p);
-  a.s_q = take(a.width_p);
-  a.s_kcur = take(a.width_p);
-  a.s_vcur = take(a.width_p);
-  a.s_attn = take(a.width_p);
-  a.s_act = take(a.ffn_p);
   a.s_hidden = take((size_t)c_.layers * c_.width);
   a.s_score = take(64);
   a.s_partial = take((size_t)c_.heads * nch * (dim_ + 2));
@@ -280,17 +301,36 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   a.error = reinterpret_cast<unsigned*>(a.scratch + a.s_score + 1);
   a.input = a.scratch + a.s_input;
 
+  // Epoch-tagged activation vectors (8 bytes per element), zeroed: tag 0 never matches
+  // because epochs start at 1.
+  uint32_t toff = 0;
+  auto ttake = [&](size_t n) {
+    uint32_t o = toff;
+    toff += (uint32_t)round_up((int)n, 64);
+    return o;
+  };
+  a.t_x = ttake(a.width_p);
+  a.t_q = ttake(a.width_p);
+  a.t_k = ttake(a.width_p);
+  a.t_v = ttake(a.width_p);
+  a.t_attn = ttake(a.width_p);
+  a.t_act = ttake(a.ffn_p);
+  a.t_done = ttake(64);
+  tagged_.alloc((size_t)toff * 8);
+  HIP_CHECK(hipMemset(tagged_.ptr, 0, (size_t)toff * 8));
+  a.tagged = reinterpret_cast<unsigned long long*>(tagged_.ptr);
+  a.tagged_bytes = toff * 8;
+
   counters_.alloc((size_t)c_.heads * 32 * 4);
   HIP_CHECK(hipMemset(counters_.ptr, 0, counters_.bytes));
   a.head_count = reinterpret_cast<unsigned*>(counters_.ptr);
   position_.alloc(8);
   HIP_CHECK(hipMemset(position_.ptr, 0, 8));
   a.position = reinterpret_cast<unsigned long long*>(position_.ptr);
-  flags_.alloc((size_t)kMaxGrid * kFlagStride * 4);
-  HIP_CHECK(hipMemset(flags_.ptr, 0, flags_.bytes));
-  a.flags = reinterpret_cast<unsigned*>(flags_.ptr);
   epoch_.alloc(64);
+  const unsigned first_epoch = 1;
   HIP_CHECK(hipMemset(epoch_.ptr, 0, 64));
+  HIP_CHECK(hipMemcpy(epoch_.ptr, &first_epoch, 4, hipMemcpyHostToDevice));
   a.epoch = reinterpret_cast<unsigned*>(epoch_.ptr);
 
   // RoPE inverse frequencies: powf(10000, -i/dim) for even i (src/cpu/Cpu.cpp:75).
@@ -306,13 +346,9 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   host_out_.alloc(64);
 
   // ---- grid
-  switch (prec_) {
-    case kFp32: legal_blocks_ = legal_blocks_t<kFp32>(); break;
-    case kMixed: legal_blocks_ = legal_blocks_t<kMixed>(); break;
-    default: legal_blocks_ = legal_blocks_t<kBf16w>(); break;
-  }
+  legal_blocks_ = dispatch([&](auto P, auto A) { return legal_blocks_t<P.value, A.value>(); });
   grid_ = options.blocks == 0 ? std::min(cus_, kMaxGrid) : options.blocks;
-  if (grid_ > kMaxGrid) throw Error(ST_ERR_INVALID, "Requested grid exceeds the barrier capacity");
+  if (grid_ > kMaxGrid) throw Error(ST_ERR_INVALID, "Requested grid exceeds " + std::to_string(kMaxGrid) + " workgroups");
   if (options.backend == ST_BACKEND_FUSED && grid_ > legal_blocks_)
     throw Error(ST_ERR_INVALID,
                 "Requested cooperative grid exceeds actual occupancy limit " + std::to_string(legal_blocks_));
@@ -341,12 +377,12 @@ Runtime::~Runtime() {
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
-template <int P>
+template <int P, int A>
 int Runtime::legal_blocks_t() {
   int per_cu = 0;
-  HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_kernel<P>, kThreads, 0));
+  HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_kernel<P, A>, kThreads, 0));
   int trace_per_cu = 0;
-  HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&trace_per_cu, trace_kernel<P>, kThreads, 0));
+  HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&trace_per_cu, trace_kernel<P, A>, kThreads, 0));
   return std::max(1, std::min(per_cu, trace_per_cu) * cus_);
 }
 
@@ -449,42 +485,34 @@ void Runtime::build_weights(const st_tensor* tensors, size_t count) {
   a.weight_bytes = (uint32_t)host.size();
 }
 
-template <int P>
+template <int P, int A>
 void Runtime::launch_phases_t() {
   const int nph = 5 * c_.layers + 2;
   for (int ph = 0; ph < nph; ph++) {
     int grid = ph == nph - 1 ? 1 : grid_;
-    hipLaunchKernelGGL(phase_kernel<P>, dim3(grid), dim3(kThreads), 0, stream_, dargs_, ph);
+    hipLaunchKernelGGL((phase_kernel<P, A>), dim3(grid), dim3(kThreads), 0, stream_, dargs_, ph);
   }
   HIP_CHECK(hipGetLastError());
 }
 
 void Runtime::launch_phases() {
-  switch (prec_) {
-    case kFp32: launch_phases_t<kFp32>(); break;
-    case kMixed: launch_phases_t<kMixed>(); break;
-    default: launch_phases_t<kBf16w>(); break;
-  }
+  dispatch([&](auto P, auto A) { launch_phases_t<P.value, A.value>(); return 0; });
 }
 
-template <int P>
-void Runtime::launch_fused_t() {
+template <int P, int A>
+void Runtime::launch_fused_t(const float* event) {
   if (grid_ == 1) {
-    hipLaunchKernelGGL(fused_kernel<P>, dim3(1), dim3(kThreads), 0, stream_, dargs_);
+    hipLaunchKernelGGL((fused_kernel<P, A>), dim3(1), dim3(kThreads), 0, stream_, dargs_, event);
   } else {
-    void* params[] = {&dargs_};
-    HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<void*>(fused_kernel<P>), dim3(grid_),
+    void* params[] = {&dargs_, &event};
+    HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<void*>(fused_kernel<P, A>), dim3(grid_),
                                          dim3(kThreads), params, 0, stream_));
   }
   HIP_CHECK(hipGetLastError());
 }
 
-void Runtime::launch_fused() {
-  switch (prec_) {
-    case kFp32: launch_fused_t<kFp32>(); break;
-    case kMixed: launch_fused_t<kMixed>(); break;
-    default: launch_fused_t<kBf16w>(); break;
-  }
+void Runtime::launch_fused(const float* event) {
+  dispatch([&](auto P, auto A) { launch_fused_t<P.value, A.value>(event); return 0; });
 }
 
 void Runtime::launch_step() {
@@ -550,13 +578,13 @@ void Runtime::snapshot(uint64_t* position, float* keys, float* values, float* hi
                         hipMemcpyDeviceToHost));
 }
 
-template <int P>
+template <int P, int A>
 void Runtime::launch_trace_t(const float* events, int count, unsigned long long* stamps) {
   if (grid_ == 1) {
-    hipLaunchKernelGGL(trace_kernel<P>, dim3(1), dim3(kThreads), 0, stream_, dargs_, events, count, stamps);
+    hipLaunchKernelGGL((trace_kernel<P, A>), dim3(1), dim3(kThreads), 0, stream_, dargs_, events, count, stamps);
   } else {
     void* params[] = {&dargs_, &events, &count, &stamps};
-    HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<void*>(trace_kernel<P>), dim3(grid_),
+    HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<void*>(trace_kernel<P, A>), dim3(grid_),
                                          dim3(kThreads), params, 0, stream_));
   }
   HIP_CHECK(hipGetLastError());
@@ -580,11 +608,8 @@ double Runtime::device_trace(const float* inputs, size_t count, double* per_even
     DeviceBuffer stamps;
     stamps.alloc((count + 1) * 8);
     const float* ev = reinterpret_cast<const float*>(trace.ptr);
-    switch (prec_) {
-      case kFp32: launch_trace_t<kFp32>(ev, (int)count, (unsigned long long*)stamps.ptr); break;
-      case kMixed: launch_trace_t<kMixed>(ev, (int)count, (unsigned long long*)stamps.ptr); break;
-      default: launch_trace_t<kBf16w>(ev, (int)count, (unsigned long long*)stamps.ptr); break;
-    }
+    auto* st_ptr = (unsigned long long*)stamps.ptr;
+    dispatch([&](auto P, auto A) { launch_trace_t<P.value, A.value>(ev, (int)count, st_ptr); return 0; });
     sync();
     std::vector<unsigned long long> st(count + 1);
     HIP_CHECK(hipMemcpy(st.data(), stamps.ptr, st.size() * 8, hipMemcpyDeviceToHost));
@@ -616,16 +641,93 @@ double Runtime::device_trace(const float* inputs, size_t count, double* per_even
   return mean;
 }
 
+// Per-launch device timing over a preloaded trace: one step per launch (FUSED: one
+// cooperative launch reading the event in place; CUDA/GRAPH: D2D staging copy + phases),
+// with a HIP event recorded on the runtime's stream after every step.
+double Runtime::device_run(const float* inputs, size_t count, bool reset_first, double* per_event) {
+  if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
+  if (!inputs || count == 0 || count > (size_t)std::numeric_limits<int>::max())
+    throw Error(ST_ERR_INVALID, "Invalid trace");
+  const int fp = args_.features_p;
+  std::vector<float> padded(count * (size_t)fp, 0.f);
+  for (size_t i = 0; i < count; i++)
+    std::memcpy(&padded[i * fp], inputs + i * c_.features, (size_t)c_.features * 4);
+  DeviceBuffer trace;
+  trace.alloc(padded.size() * 4);
+  HIP_CHECK(hipMemcpy(trace.ptr, padded.data(), padded.size() * 4, hipMemcpyHostToDevice));
+  if (reset_first) reset();
+  std::vector<hipEvent_t> ev(count + 1);
+  for (auto& e : ev) HIP_CHECK(hipEventCreate(&e));
+  const float* base = reinterpret_cast<const float*>(trace.ptr);
+  HIP_CHECK(hipEventRecord(ev[0], stream_));
+  for (size_t i = 0; i < count; i++) {
+    if (opt_.backend == ST_BACKEND_FUSED) {
+      launch_fused(base + i * fp);
+    } else {
+      HIP_CHECK(hipMemcpyAsync(args_.scratch + args_.s_input, base + i * fp, (size_t)fp * 4,
+                               hipMemcpyDeviceToDevice, stream_));
+      launch_step();
+    }
+    HIP_CHECK(hipEventRecord(ev[i + 1], stream_));
+  }
+  sync();
+  double total_ms = 0;
+  for (size_t i = 0; i < count; i++) {
+    float ms = 0;
+    HIP_CHECK(hipEventElapsedTime(&ms, ev[i], ev[i + 1]));
+    if (per_event) per_event[i] = ms * 1000.0;
+    total_ms += ms;
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  check_device_error();
+  return total_ms * 1000.0 / count;
+}
+
+// One fused step with wall-clock stamps from workgroup 0. For each phase writes four
+// times in microseconds since the step started: phase start (all waves released), first
+// stream wave done with the phase, control wave starts staging the next phase's inputs,
+// staging done (0 where not recorded); then the end of the step.
+size_t Runtime::phase_times(const float* input, double* us, size_t cap) {
+  if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
+  if (opt_.backend != ST_BACKEND_FUSED) throw Error(ST_ERR_INVALID, "Phase stamps require the fused backend");
+  const int nph = 5 * c_.layers + 2;
+  const size_t n = (size_t)4 * nph + 1;
+  DeviceBuffer stamps, args;
+  stamps.alloc(n * 8);
+  HIP_CHECK(hipMemset(stamps.ptr, 0, n * 8));
+  StepArgs prof = args_;
+  prof.stamps = reinterpret_cast<unsigned long long*>(stamps.ptr);
+  args.alloc(sizeof(StepArgs));
+  HIP_CHECK(hipMemcpy(args.ptr, &prof, sizeof(StepArgs), hipMemcpyHostToDevice));
+  std::memcpy(host_in_.ptr, input, (size_t)c_.features * 4);
+  HIP_CHECK(hipMemcpyAsync(args_.scratch + args_.s_input, host_in_.ptr, (size_t)args_.features_p * 4,
+                           hipMemcpyHostToDevice, stream_));
+  const StepArgs* saved = dargs_;
+  dargs_ = reinterpret_cast<const StepArgs*>(args.ptr);
+  try {
+    launch_fused();
+    sync();
+  } catch (...) {
+    dargs_ = saved;
+    throw;
+  }
+  dargs_ = saved;
+  check_device_error();
+  std::vector<unsigned long long> st(n);
+  HIP_CHECK(hipMemcpy(st.data(), stamps.ptr, n * 8, hipMemcpyDeviceToHost));
+  for (size_t i = 0; i < n && i < cap; i++)
+    us[i] = st[i] ? (double)(long long)(st[i] - st[0]) * 1000.0 / wall_khz_ : 0.0;
+  return n;
+}
+
 std::string Runtime::info() {
   hipFuncAttributes fa{};
   const void* fn = nullptr;
   std::string name;
   bool fused = opt_.backend == ST_BACKEND_FUSED;
-  switch (prec_) {
-    case kFp32: fn = fused ? (const void*)fused_kernel<kFp32> : (const void*)phase_kernel<kFp32>; break;
-    case kMixed: fn = fused ? (const void*)fused_kernel<kMixed> : (const void*)phase_kernel<kMixed>; break;
-    default: fn = fused ? (const void*)fused_kernel<kBf16w> : (const void*)phase_kernel<kBf16w>; break;
-  }
+  fn = dispatch([&](auto P, auto A) {
+    return fused ? (const void*)fused_kernel<P.value, A.value> : (const void*)phase_kernel<P.value, A.value>;
+  });
   name = fused ? "fused_kernel" : "phase_kernel";
   HIP_CHECK(hipFuncGetAttributes(&fa, fn));
   static const char* backends[] = {"cuda(staged)", "graph", "cublas", "cublas-graph", "fused", "persistent"};
@@ -639,7 +741,8 @@ std::string Runtime::info() {
     << ", \"phases_per_step\": " << 5 * c_.layers + 2 << ", \"prefetch_slabs\": " << kPF
     << ", \"attention_chunk\": " << args_.chunk << ", \"weight_arena_bytes\": " << args_.weight_bytes
     << ", \"matvec_implementation\": \"wave64 16-byte buffer loads, register ring, butterfly reduction\""
-    << ", \"attention_implementation\": \"LDS-staged window chunks, last-arriver head combine\""
+    << ", \"attention_implementation\": \"" << (args_.attn_regs ? "register" : "LDS-staged")
+    << " window chunks, last-arriver head combine\""
     << ", \"transport\": \"pinned-copy-stream-sync\""
     << ", \"weights_and_kv_storage\": \""
     << (prec_ == kMixed ? "FP16/FP16" : prec_ == kBf16w ? "BF16/FP32" : "FP32/FP32") << "\"}";
@@ -749,6 +852,22 @@ int st_runtime_device_trace(st_runtime* r, const float* inputs, size_t count, do
   return guarded([&] {
     if (!r || !us_per_event) throw stamd::Error(ST_ERR_INVALID, "Null argument");
     *us_per_event = r->impl->device_trace(inputs, count, per_event_us);
+  });
+}
+
+int st_runtime_device_run(st_runtime* r, const float* inputs, size_t count, int32_t reset,
+                          double* us_per_event, double* per_event_us) {
+  return guarded([&] {
+    if (!r || !us_per_event) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    *us_per_event = r->impl->device_run(inputs, count, reset != 0, per_event_us);
+  });
+}
+
+int st_runtime_phase_times(st_runtime* r, const float* input, double* us, size_t cap, size_t* count) {
+  return guarded([&] {
+    if (!r || !input || (!us && cap)) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    size_t n = r->impl->phase_times(input, us, cap);
+    if (count) *count = n;
   });
 }
 

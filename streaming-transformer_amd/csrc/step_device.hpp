@@ -34,8 +34,7 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kStreamWaves = kWaves - 1;
 constexpr int kPF = 16;            // register ring depth (slabs) per stream wave
-constexpr int kFlagStride = 32;    // u32 words between barrier flags (128 B)
-constexpr int kMaxGrid = 1024;     // workgroups supported by the barrier poll
+constexpr int kMaxGrid = 1024;     // largest grid accepted
 constexpr int kMaxLayers = 16;
 constexpr int kXs = 4096 + 64;     // LDS activation vector capacity (floats)
 constexpr int kAttnLds = 2304;     // per stream wave K/V staging (floats): CH*(dh+4) <= 2304
@@ -43,7 +42,7 @@ constexpr int kMaxDim = 1024;
 
 enum Precision : int { kFp32 = 0, kMixed = 1, kBf16w = 2 };
 enum PhaseKind : int { kInput = 0, kQkv, kAttn, kOut, kGateUp, kDown, kFinal };
-enum ErrorBits : unsigned { kErrBarrierTimeout = 1u, kErrMailboxTimeout = 2u };
+enum ErrorBits : unsigned { kErrPollTimeout = 1u, kErrMailboxTimeout = 2u };
 
 // Buffer-resource dword3 for raw buffer access on gfx9 (32-bit data format).
 constexpr int kRsrcWord3 = 0x00020000;
@@ -54,13 +53,14 @@ struct LayerWeights {
   uint32_t norm1, norm2, qkv, out, gateup, down;  // byte offsets into the weight arena
 };
 
-// Kernel argument block (passed by value; ~0.9 KB).
+// Step arguments, kept in device memory and read through a restrict pointer (~0.6 KB).
 struct StepArgs {
   // shape
   int layers, width, heads, ffn, window, features, dim;
   float epsilon;
   int width_p, ffn_p, features_p;  // padded row lengths (elements), multiples of 16 B
   int chunk;                       // attention slots per work item
+  int attn_regs;                   // 1: head dim suits the register attention path
   int grid;                        // workgroups in this launch
   // weights (one arena, byte offsets)
   const char* weights;
@@ -73,16 +73,20 @@ struct StepArgs {
   uint32_t cache_bytes;            // bytes of one of keys/values
   float* scratch;                  // fp32 scratch arena (agent-coherent access)
   uint32_t scratch_bytes;
-  // scratch offsets (floats)
-  uint32_t s_input, s_x, s_q, s_kcur, s_vcur, s_attn, s_act, s_hidden, s_score, s_partial;
-  unsigned* head_count;            // [H] * 32 words apart
+  // scratch offsets (floats): host-staged input, hidden state, score, attention partials
+  uint32_t s_input, s_hidden, s_score, s_partial;
+  // tagged vectors (8-byte elements: epoch << 32 | float bits)
+  unsigned long long* tagged;
+  uint32_t tagged_bytes;
+  uint32_t t_x, t_q, t_k, t_v, t_attn, t_act, t_done;  // element offsets
+  unsigned* head_count;            // [H] * 32 words apart (wrapping chunk counters)
   unsigned long long* position;
-  unsigned* flags;                 // barrier flags [grid * kFlagStride]
-  unsigned* epoch;                 // persistent epoch base (fused launches)
+  unsigned* epoch;                 // epoch of phase 0 of the next step
   unsigned* error;                 // sticky error bits
   const float* rope_freq;          // [dh/2]
   const float* input;              // event source for the INPUT phase (device memory)
-  unsigned long long spin_limit;   // barrier timeout in wall-clock ticks
+  unsigned long long spin_limit;   // poll timeout in wall-clock ticks
+  unsigned long long* stamps;      // optional per-phase wall-clock stamps (workgroup 0)
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -241,30 +245,14 @@ __device__ __forceinline__ Mv matvec_of(const StepArgs& a, Phase p) {
 }
 
 // Work of one stream wave in a matvec phase. Rows are padded to whole slabs (1 KiB), so
-// the U rows of a unit form U*S consecutive slabs; the wave owns units wid, wid + nw, ...
+// the U rows of a unit form U*S consecutive slabs.
 struct WaveWork {
-  int wid, nw;          // wave index among all stream waves, number of stream waves
   int slabs_row;        // slabs per row (S)
   int per_unit;         // slabs per unit (U*S)
   int slabs;            // total slabs owned by this wave
   uint32_t base;        // byte offset of the first owned unit
   uint32_t unit_stride; // bytes between consecutive owned units
 };
-
-template <int P>
-__device__ __forceinline__ WaveWork work_of(const StepArgs& a, const Mv& m, int grid, int g, int sw) {
-  WaveWork w;
-  w.nw = grid * kStreamWaves;
-  w.wid = g + grid * sw;
-  int total_units = m.rows / m.unit;
-  int units = total_units > w.wid ? (total_units - w.wid + w.nw - 1) / w.nw : 0;
-  w.slabs_row = m.cols_p * Traits<P>::kWBytes / 1024;
-  w.per_unit = m.unit * w.slabs_row;
-  w.slabs = units * w.per_unit;
-  w.base = m.woff + (uint32_t)w.wid * (uint32_t)w.per_unit * 1024u;
-  w.unit_stride = (uint32_t)w.nw * (uint32_t)w.per_unit * 1024u;
-  return w;
-}
 
 // Incremental cursor over a wave's slab stream (all fields wave-uniform).
 struct SlabCursor {

@@ -1,112 +1,305 @@
-// Phase bodies, grid barrier and kernels. Included once by runtime.hip.
+// Phase bodies and kernels. Included once by runtime.hip.
+//
+// Cross-workgroup dataflow uses epoch-tagged vectors: every element of x, q, k, v, attn and
+// act is one 8-byte word (epoch << 32 | float bits), written with a single write-through
+// store and read with agent-coherent loads. A consumer polls the elements it needs until
+// every tag equals the epoch of the producing phase, so there is no grid barrier, no store
+// acknowledgement wait before publishing and no separate staging round trip. Each phase p
+// of a step has epoch base + p; base advances by phases + 1 per step.
+//
+// Reuse safety: a tagged vector is overwritten only in a phase whose writers have
+// consumed outputs that every reader of the previous value produced after its read
+// (x: INPUT/OUT/DOWN, q/k/v: QKV, attn: ATTN, act: GATEUP), so no reader can observe a
+// newer epoch than the one it waits for. Workgroups without work in a phase skip its
+// reads. The K/V ring row of the current slot is written by the attention item that owns
+// the slot, before that item's partial is counted, so the row is complete before anything
+// downstream of the attention output runs.
 #pragma once
 
 #include "step_device.hpp"
 
 namespace stamd {
 
-struct LdsAll : Lds {
-  float xres[kMaxDim];          // residual input x for OUT/DOWN epilogues
+struct LdsAll {
+  float xs[2][kXs];                      // phase input vector, double buffered by phase parity
+  float xres[2][kMaxDim];                // own rows of x for the OUT/DOWN residuals
+  float qkv[3 * kMaxDim];                // attention LDS path: q, k, v of the step
+  float stage[kStreamWaves][kAttnLds];   // attention LDS path: per-wave K/V staging; combine scale
   float probs[kStreamWaves][64];
+  float sums[kStreamWaves][kPF][2];      // row sums of units finished in the current ring pass
+  float rope[kMaxDim / 2];               // RoPE inverse frequencies
+  unsigned done[2];                      // stream waves finished with the phase of this parity
 };
 
 template <int P>
 struct Ctx {
   const StepArgs& a;
   LdsAll& lds;
-  __amdgpu_buffer_rsrc_t wr, kr, vr, sr;
-  int g, lane, wave;
-  unsigned long long t;
+  __amdgpu_buffer_rsrc_t wr, kr, vr, sr, tr;
+  int g, grid, lane, wave;
+  unsigned long long t;  // position of the step
   int valid, slot;
-  const float* input;  // event read by the INPUT phase
+  unsigned base;         // epoch of phase 0 of this step
+  bool dead;             // a poll timed out; stop waiting
+  const float* input;    // event read by the INPUT phase
 
-  __device__ __forceinline__ Ctx(const StepArgs& args, LdsAll& l, int grid_index)
-      : a(args), lds(l), g(grid_index), lane(lane_id()), wave(wave_id()), t(0), valid(0), slot(0),
-        input(args.input) {
+  __device__ __forceinline__ Ctx(const StepArgs& args, LdsAll& l, int grid_index, int grid_size)
+      : a(args), lds(l), g(grid_index), grid(grid_size), lane(lane_id()), wave(wave_id()), t(0), valid(0),
+        slot(0), base(0), dead(false), input(args.input) {
     wr = make_rsrc(a.weights, a.weight_bytes);
     kr = make_rsrc(a.keys, a.cache_bytes);
     vr = make_rsrc(a.values, a.cache_bytes);
     sr = make_rsrc(a.scratch, a.scratch_bytes);
+    tr = make_rsrc(a.tagged, a.tagged_bytes);
   }
   __device__ __forceinline__ void set_position(unsigned long long pos) {
     t = pos;
     valid = pos + 1 < (unsigned long long)a.window ? (int)(pos + 1) : a.window;
     slot = (int)(pos % (unsigned long long)a.window);
   }
+  __device__ __forceinline__ unsigned epoch(int ph) const { return base + (unsigned)ph; }
   __device__ __forceinline__ float sload(uint32_t index) { return ld4_coherent(sr, index * 4u); }
   __device__ __forceinline__ void sstore(uint32_t index, float v) { st4_coherent(sr, index * 4u, v); }
+  // Publish one element of a tagged vector.
+  __device__ __forceinline__ void tstore(uint32_t index, unsigned ep, float v) {
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    v2i w = {__builtin_bit_cast(int, v), (int)ep};
+    __builtin_amdgcn_raw_buffer_store_b64(w, tr, (int)(index * 8u), 0, kSc1);
+  }
+  __device__ __forceinline__ void timeout() {
+    if (lane == 0) __hip_atomic_fetch_or(a.error, kErrPollTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    dead = true;
+  }
 };
 
 __device__ __forceinline__ unsigned long long load_position(const StepArgs& a) {
   return __hip_atomic_load(a.position, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ unsigned load_epoch(const StepArgs& a) {
+  return __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Phase indices within a step.
+__device__ __forceinline__ int ph_index(int kind, int layer) { return kind == kInput ? 0 : 1 + 5 * layer + (kind - kQkv); }
+__device__ __forceinline__ int ph_final(const StepArgs& a) { return 1 + 5 * a.layers; }
+// Phase that last wrote x before `layer`'s QKV phase.
+__device__ __forceinline__ int ph_x_before(int layer) { return layer == 0 ? 0 : ph_index(kDown, layer - 1); }
+
+// ---------------------------------------------------------------------------------------------
+// polling tagged vectors
+
+constexpr int kPollSleep = 2;  // s_sleep units (64 clocks each) between failed polls
+
+// Wait until elements [2*p0, 2*(p0+np)) of tagged vector `tv` carry epoch `ep` (elements at or
+// beyond `n` are padding and are not checked), then write their values (0 for padding) to
+// dst[0 ..). One wave; NP 16-byte pieces per lane per pass.
+template <int P, int NP>
+__device__ __forceinline__ void poll_pieces(Ctx<P>& c, uint32_t tv, int n, int p0, int np, unsigned ep, float* dst) {
+  uint4 buf[NP];
+  unsigned long long start = wall_clock64();
+  while (true) {
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+      int pc = c.lane + 64 * k;
+      int pcl = pc < np ? pc : np - 1;
+      buf[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             c.tr, (int)((tv + 2u * (uint32_t)(p0 + pcl)) * 8u), 0, kSc1));
+    }
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+      int pc = c.lane + 64 * k;
+      int e0 = 2 * (p0 + pc);
+      bool in = pc < np;
+      ok = ok && (!in || ((e0 >= n || buf[k].y == ep) && (e0 + 1 >= n || buf[k].w == ep)));
+    }
+    if (__all(ok) || c.dead) break;
+    if (wall_clock64() - start > c.a.spin_limit) {
+      c.timeout();
+      break;
+    }
+    __builtin_amdgcn_s_sleep(kPollSleep);
+  }
+#pragma unroll
+  for (int k = 0; k < NP; k++) {
+    int pc = c.lane + 64 * k;
+    int e0 = 2 * (p0 + pc);
+    if (pc < np) {
+      dst[2 * pc] = e0 < n ? __builtin_bit_cast(float, buf[k].x) : 0.f;
+      dst[2 * pc + 1] = e0 + 1 < n ? __builtin_bit_cast(float, buf[k].z) : 0.f;
+    }
+  }
+}
+
+// Whole vector of n elements padded to n_p (a multiple of 256) into dst[0 .. n_p).
+template <int P>
+__device__ __forceinline__ void poll_vector(Ctx<P>& c, uint32_t tv, int n, int n_p, unsigned ep, float* dst) {
+  const int pieces = n_p / 2;
+  if (pieces <= 512) {
+    poll_pieces<P, 8>(c, tv, n, 0, pieces, ep, dst);
+  } else {
+    for (int p0 = 0; p0 < pieces; p0 += 1024)
+      poll_pieces<P, 16>(c, tv, n, p0, pieces - p0 < 1024 ? pieces - p0 : 1024, ep, dst + 2 * p0);
+  }
+}
+
+// Elements [first, first + count) of tagged vector `tv` into dst[0 .. count).
+template <int P>
+__device__ __forceinline__ void poll_range(Ctx<P>& c, uint32_t tv, int first, int count, unsigned ep, float* dst) {
+  constexpr int NE = 4;
+  for (int e0 = 0; e0 < count; e0 += 64 * NE) {
+    uint2 buf[NE];
+    unsigned long long start = wall_clock64();
+    while (true) {
+#pragma unroll
+      for (int k = 0; k < NE; k++) {
+        int e = e0 + c.lane + 64 * k;
+        int el = e < count ? e : count - 1;
+        buf[k] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                               c.tr, (int)((tv + (uint32_t)(first + el)) * 8u), 0, kSc1));
+      }
+      bool ok = true;
+#pragma unroll
+      for (int k = 0; k < NE; k++) ok = ok && (e0 + c.lane + 64 * k >= count || buf[k].y == ep);
+      if (__all(ok) || c.dead) break;
+      if (wall_clock64() - start > c.a.spin_limit) {
+        c.timeout();
+        break;
+      }
+      __builtin_amdgcn_s_sleep(kPollSleep);
+    }
+#pragma unroll
+    for (int k = 0; k < NE; k++) {
+      int e = e0 + c.lane + 64 * k;
+      if (e < count) dst[e] = __builtin_bit_cast(float, buf[k].x);
+    }
+  }
+}
 
 // ---------------------------------------------------------------------------------------------
 // control wave: stage phase inputs into LDS
 
-// Copy n floats (n padded to a multiple of 4 in scratch) from scratch into LDS.
+// RMSNorm in place over v[0 .. width) (src/cuda/Primitives.cuh:122-135):
+// s = 1/sqrt(sum(v^2)/d + eps), v = cast(v * s * w).
 template <int P>
-__device__ __forceinline__ void stage_vector(Ctx<P>& c, uint32_t src, int n_p, float* dst) {
-  for (int i = c.lane * 4; i < n_p; i += 256) {
-    float4 v = ld16_coherent(c.sr, (src + (uint32_t)i) * 4u);
-    *reinterpret_cast<float4*>(dst + i) = v;
-  }
-}
-
-// RMSNorm of the width-vector in dst (in place), src/cuda/Primitives.cuh:122-135.
-template <int P>
-__device__ __forceinline__ void norm_in_place(Ctx<P>& c, float* v, uint32_t w_off) {
+__device__ __forceinline__ void norm_in_lds(Ctx<P>& c, float* v, uint32_t w_off) {
   const int d = c.a.width;
+  constexpr int K = kMaxDim / 64;
+  float w[K];
+#pragma unroll
+  for (int k = 0; k < K; k++) {
+    int i = c.lane + 64 * k;
+    w[k] = load_weight_scalar<P>(c.wr, w_off, i < d ? i : d - 1);
+  }
   float sum = 0.f;
-  for (int i = c.lane; i < d; i += 64) sum += v[i] * v[i];
+#pragma unroll
+  for (int k = 0; k < K; k++) {
+    int i = c.lane + 64 * k;
+    if (i < d) sum += v[i] * v[i];
+  }
   sum = wave_sum(sum);
-  float scale = 1.0f / sqrtf(sum / (float)d + c.a.epsilon);
-  for (int i = c.lane; i < d; i += 64) {
-    float w = load_weight_scalar<P>(c.wr, w_off, i);
-    v[i] = cast<P>(v[i] * scale * w);
+  const float scale = 1.0f / sqrtf(sum / (float)d + c.a.epsilon);
+#pragma unroll
+  for (int k = 0; k < K; k++) {
+    int i = c.lane + 64 * k;
+    if (i < d) v[i] = cast<P>(v[i] * scale * w[k]);
   }
 }
 
+// Units of a matvec phase owned by workgroup g: [first, first + count).
+struct Own {
+  int first, count;
+};
+
 template <int P>
-__device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p) {
+__device__ __forceinline__ Own own_units(const Mv& m, int grid, int g) {
+  int total = m.rows / m.unit;
+  int per = (total + grid - 1) / grid;
+  int first = g * per;
+  int end = first + per < total ? first + per : total;
+  return {first, end > first ? end - first : 0};
+}
+
+template <int P, int A>
+__device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p, int buf) {
   const StepArgs& a = c.a;
-  switch (p.kind) {
-    case kInput: {
-      __amdgpu_buffer_rsrc_t ir = make_rsrc(c.input, (uint32_t)a.features_p * 4u);
-      for (int i = c.lane * 4; i < a.features_p; i += 256)
-        *reinterpret_cast<float4*>(c.lds.xs + i) = ld16_coherent(ir, (uint32_t)i * 4u);
-      break;
+  float* xs = c.lds.xs[buf];
+  // What to poll: up to three whole vectors, an optional range of own rows, an optional norm.
+  uint32_t vec[3];
+  float* dst[3];
+  int nvec = 0, n = a.width, n_p = a.width_p;
+  unsigned ep = 0, ep_own = 0;
+  uint32_t norm_w = 0;
+  bool norm = false;
+  Own own{0, 0};
+  if (p.kind == kAttn) {
+    if constexpr (A == 1) return;
+    ep = c.epoch(ph_index(kQkv, p.layer));
+    vec[0] = a.t_q; dst[0] = c.lds.qkv;
+    vec[1] = a.t_k; dst[1] = c.lds.qkv + kMaxDim;
+    vec[2] = a.t_v; dst[2] = c.lds.qkv + 2 * kMaxDim;
+    nvec = 3;
+  } else if (p.kind == kFinal) {
+    if (c.g != 0) return;
+    ep = c.epoch(ph_index(kDown, a.layers - 1));
+    vec[0] = a.t_x; dst[0] = xs; nvec = 1;
+    norm = true; norm_w = a.w_final_norm;
+  } else {
+    Mv m = matvec_of<P>(a, p);
+    Own mine = own_units<P>(m, c.grid, c.g);
+    if (mine.count == 0) return;
+    switch (p.kind) {
+      case kInput: {
+        __amdgpu_buffer_rsrc_t ir = make_rsrc(c.input, (uint32_t)a.features_p * 4u);
+        for (int i = c.lane * 4; i < a.features_p; i += 256)
+          *reinterpret_cast<float4*>(xs + i) = ld16_coherent(ir, (uint32_t)i * 4u);
+        return;
+      }
+      case kQkv:
+        ep = c.epoch(ph_x_before(p.layer));
+        vec[0] = a.t_x; dst[0] = xs; nvec = 1;
+        norm = true; norm_w = a.layer[p.layer].norm1;
+        break;
+      case kOut:
+        ep = c.epoch(ph_index(kAttn, p.layer));
+        vec[0] = a.t_attn; dst[0] = xs; nvec = 1;
+        own = mine; ep_own = c.epoch(ph_x_before(p.layer));
+        break;
+      case kGateUp:
+        ep = c.epoch(ph_index(kOut, p.layer));
+        vec[0] = a.t_x; dst[0] = xs; nvec = 1;
+        norm = true; norm_w = a.layer[p.layer].norm2;
+        break;
+      default:  // kDown
+        ep = c.epoch(ph_index(kGateUp, p.layer));
+        vec[0] = a.t_act; dst[0] = xs; nvec = 1;
+        n = a.ffn; n_p = a.ffn_p;
+        own = mine; ep_own = c.epoch(ph_index(kOut, p.layer));
+        break;
     }
-    case kQkv:
-      stage_vector(c, a.s_x, a.width_p, c.lds.xs);
-      norm_in_place(c, c.lds.xs, a.layer[p.layer].norm1);
-      break;
-    case kAttn:
-      stage_vector(c, a.s_q, a.width_p, c.lds.qkv);
-      stage_vector(c, a.s_kcur, a.width_p, c.lds.qkv + kMaxDim);
-      stage_vector(c, a.s_vcur, a.width_p, c.lds.qkv + 2 * kMaxDim);
-      break;
-    case kOut:
-      stage_vector(c, a.s_attn, a.width_p, c.lds.xs);
-      stage_vector(c, a.s_x, a.width_p, c.lds.xres);
-      break;
-    case kGateUp:
-      stage_vector(c, a.s_x, a.width_p, c.lds.xs);
-      norm_in_place(c, c.lds.xs, a.layer[p.layer].norm2);
-      break;
-    case kDown:
-      stage_vector(c, a.s_act, a.ffn_p, c.lds.xs);
-      stage_vector(c, a.s_x, a.width_p, c.lds.xres);
-      break;
-    case kFinal:
-      stage_vector(c, a.s_x, a.width_p, c.lds.xs);
-      norm_in_place(c, c.lds.xs, a.w_final_norm);
-      break;
   }
+  for (int v = 0; v < nvec; v++) poll_vector(c, vec[v], n, n_p, ep, dst[v]);
+  if (own.count) poll_range(c, a.t_x, own.first, own.count, ep_own, c.lds.xres[buf]);
+  if (norm) norm_in_lds(c, xs, norm_w);
 }
 
 // ---------------------------------------------------------------------------------------------
 // stream waves: matvec phases
+
+// Work of stream wave sw: units first + sw, first + sw + 7, ... within the workgroup's block.
+template <int P>
+__device__ __forceinline__ WaveWork work_of(const Mv& m, int grid, int g, int sw, int& unit0) {
+  Own own = own_units<P>(m, grid, g);
+  WaveWork w;
+  w.slabs_row = m.cols_p * Traits<P>::kWBytes / 1024;
+  w.per_unit = m.unit * w.slabs_row;
+  int units = own.count > sw ? (own.count - sw + kStreamWaves - 1) / kStreamWaves : 0;
+  unit0 = own.first + sw;
+  w.slabs = units * w.per_unit;
+  w.base = m.woff + (uint32_t)unit0 * (uint32_t)w.per_unit * 1024u;
+  w.unit_stride = (uint32_t)kStreamWaves * (uint32_t)w.per_unit * 1024u;
+  return w;
+}
 
 template <int P>
 __device__ __forceinline__ void prefetch_matvec(Ctx<P>& c, const WaveWork& w, uint4 (&ring)[kPF]) {
@@ -120,7 +313,7 @@ __device__ __forceinline__ void prefetch_matvec(Ctx<P>& c, const WaveWork& w, ui
   }
 }
 
-// Attention work item geometry.
+// Attention work items (head, chunk of the window) over all stream waves of the grid.
 struct AttnWork {
   int wid, nw, items, nch;  // items owned by this wave; chunks per head
   int kchunks;              // 16-byte chunks of one K (or V) block
@@ -140,103 +333,77 @@ __device__ __forceinline__ AttnWork attn_work(const StepArgs& a, int grid, int g
 
 // Byte offset of the kk-th 16-byte chunk of the K/V block of item (h, ch), clamped.
 template <int P>
-__device__ __forceinline__ uint32_t attn_chunk_offset(const StepArgs& a, int layer, int h, int ch, int kk,
-                                             int kchunks) {
+__device__ __forceinline__ uint32_t attn_chunk_offset(const StepArgs& a, int layer, int h, int ch, int kk, int kchunks) {
   int k = kk < kchunks ? kk : kchunks - 1;
   uint32_t row0 = ((uint32_t)(layer * a.heads + h) * (uint32_t)a.window + (uint32_t)(ch * a.chunk));
   return row0 * (uint32_t)a.dim * Traits<P>::kKvBytes + (uint32_t)k * 16u;
 }
 
 template <int P>
-__device__ __forceinline__ void prefetch_attn(Ctx<P>& c, int layer, const AttnWork& w, uint4 (&ring)[kPF]) {
-  if (w.items == 0) return;
-  int it = w.wid;
-  int h = it / w.nch, ch = it - h * w.nch;
-  // K block chunks at ring[0..kPF/2), V block at ring[kPF/2..kPF)
+__device__ __forceinline__ void load_block(Ctx<P>& c, __amdgpu_buffer_rsrc_t r, int layer, int h, int ch, int kchunks,
+                                           uint4* part) {
 #pragma unroll
-  for (int j = 0; j < kPF / 2; j++) {
-    uint32_t off = attn_chunk_offset<P>(c.a, layer, h, ch, c.lane + 64 * j, w.kchunks);
-    ring[j] = ld16(c.kr, off);
-    ring[kPF / 2 + j] = ld16(c.vr, off);
-  }
+  for (int j = 0; j < kPF / 2; j++) part[j] = ld16(r, attn_chunk_offset<P>(c.a, layer, h, ch, c.lane + 64 * j, kchunks));
 }
 
 template <int P>
-__device__ __forceinline__ void prefetch(Ctx<P>& c, Phase p, int grid, uint4 (&ring)[kPF]) {
+__device__ __forceinline__ void prefetch(Ctx<P>& c, Phase p, uint4 (&ring)[kPF]) {
   int sw = c.wave - 1;
   if (p.kind == kAttn) {
-    AttnWork w = attn_work<P>(c.a, grid, c.g, sw);
-    prefetch_attn(c, p.layer, w, ring);
+    AttnWork w = attn_work<P>(c.a, c.grid, c.g, sw);
+    if (w.items == 0) return;
+    int h = w.wid / w.nch, ch = w.wid - h * w.nch;
+    load_block<P>(c, c.kr, p.layer, h, ch, w.kchunks, ring);
+    load_block<P>(c, c.vr, p.layer, h, ch, w.kchunks, ring + kPF / 2);
   } else if (p.kind != kFinal) {
     Mv m = matvec_of<P>(c.a, p);
-    WaveWork w = work_of<P>(c.a, m, grid, c.g, sw);
+    int unit0;
+    WaveWork w = work_of<P>(m, c.grid, c.g, sw, unit0);
     prefetch_matvec(c, w, ring);
   }
 }
 
-// Epilogue of one unit (lane 0 only). s0/s1 are the row sums.
+// Epilogue of one unit (lane 0 only); s0/s1 are the row sums, xres the own rows of x.
 template <int P>
-__device__ __forceinline__ void epilogue(Ctx<P>& c, Phase p, int unit, float s0, float s1) {
+__device__ __forceinline__ void epilogue(Ctx<P>& c, Phase p, int unit, float s0, float s1, const float* xres, int first) {
   const StepArgs& a = c.a;
+  const unsigned ep = c.epoch(ph_index(p.kind, p.layer));
   switch (p.kind) {
     case kInput:
-      c.sstore(a.s_x + unit, cast<P>(s0));
+      c.tstore(a.t_x + unit, ep, cast<P>(s0));
       break;
     case kQkv: {
       int r0 = unit * 2;
       int sec = r0 / a.width;
       int i = r0 - sec * a.width;
       float va = cast<P>(s0), vb = cast<P>(s1);
-      int h = i / a.dim;
-      int e = i - h * a.dim;
-      uint32_t kv = ((uint32_t)(p.layer * a.heads + h) * (uint32_t)a.window + (uint32_t)c.slot) *
-                        (uint32_t)a.dim + (uint32_t)e;
       if (sec < 2) {
         // RoPE on the adjacent pair (i, i+1), src/cuda/Primitives.cuh:148-159
-        float angle = (float)c.t * a.rope_freq[e >> 1];
+        int e = i % a.dim;
+        float angle = (float)c.t * c.lds.rope[e >> 1];
         float co = cosf(angle), si = sinf(angle);
         float ra = cast<P>(va * co - vb * si);
         float rb = cast<P>(va * si + vb * co);
-        if (sec == 0) {
-          c.sstore(a.s_q + i, ra);
-          c.sstore(a.s_q + i + 1, rb);
-        } else {
-          c.sstore(a.s_kcur + i, ra);
-          c.sstore(a.s_kcur + i + 1, rb);
-          if constexpr (P == kMixed) {
-            st2_coherent(c.kr, kv * 2u, float_to_half(ra));
-            st2_coherent(c.kr, kv * 2u + 2u, float_to_half(rb));
-          } else {
-            st4_coherent(c.kr, kv * 4u, ra);
-            st4_coherent(c.kr, kv * 4u + 4u, rb);
-          }
-        }
+        uint32_t tv = sec == 0 ? a.t_q : a.t_k;
+        c.tstore(tv + i, ep, ra);
+        c.tstore(tv + i + 1, ep, rb);
       } else {
-        c.sstore(a.s_vcur + i, va);
-        c.sstore(a.s_vcur + i + 1, vb);
-        if constexpr (P == kMixed) {
-          st2_coherent(c.vr, kv * 2u, float_to_half(va));
-          st2_coherent(c.vr, kv * 2u + 2u, float_to_half(vb));
-        } else {
-          st4_coherent(c.vr, kv * 4u, va);
-          st4_coherent(c.vr, kv * 4u + 4u, vb);
-        }
+        c.tstore(a.t_v + i, ep, va);
+        c.tstore(a.t_v + i + 1, ep, vb);
       }
       break;
     }
-    case kOut: {
-      float v = cast<P>(c.lds.xres[unit] + cast<P>(s0));
-      c.sstore(a.s_x + unit, v);
+    case kOut:
+      c.tstore(a.t_x + unit, ep, cast<P>(xres[unit - first] + cast<P>(s0)));
       break;
-    }
     case kGateUp: {
       float gv = cast<P>(s0), uv = cast<P>(s1);
-      c.sstore(a.s_act + unit, cast<P>((gv / (1.0f + expf(-gv))) * uv));
+      c.tstore(a.t_act + unit, ep, cast<P>((gv / (1.0f + expf(-gv))) * uv));
       break;
     }
     case kDown: {
-      float v = cast<P>(c.lds.xres[unit] + cast<P>(s0));
-      c.sstore(a.s_x + unit, v);
+      float v = cast<P>(xres[unit - first] + cast<P>(s0));
+      c.tstore(a.t_x + unit, ep, v);
       c.sstore(a.s_hidden + (uint32_t)p.layer * a.width + unit, v);
       break;
     }
@@ -246,16 +413,20 @@ __device__ __forceinline__ void epilogue(Ctx<P>& c, Phase p, int unit, float s0,
 }
 
 template <int P>
-__device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, int grid, uint4 (&ring)[kPF]) {
+__device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* xs_buf, const float* xres,
+                                               uint4 (&ring)[kPF]) {
   Mv m = matvec_of<P>(c.a, p);
-  WaveWork w = work_of<P>(c.a, m, grid, c.g, c.wave - 1);
+  int unit;
+  WaveWork w = work_of<P>(m, c.grid, c.g, c.wave - 1, unit);
   if (w.slabs == 0) return;
+  const int first = own_units<P>(m, c.grid, c.g).first;
+  float (*sums)[2] = c.lds.sums[c.wave - 1];
   SlabCursor refill = cursor_at(w, kPF);
-  int unit = w.wid;  // global unit index of the unit being reduced
-  int ru = 0, s = 0; // row within the unit, slab within the row
+  int ru = 0, s = 0;  // row within the unit, slab within the row
   float acc0 = 0.f, acc1 = 0.f;
-  const float* xs = c.lds.xs + c.lane * Traits<P>::kEpc;
+  const float* xs = xs_buf + c.lane * Traits<P>::kEpc;
   for (int base = 0; base < w.slabs; base += kPF) {
+    int finished = 0;  // units completed in this pass of the ring
 #pragma unroll
     for (int j = 0; j < kPF; j++) {
       if (base + j < w.slabs) {
@@ -271,19 +442,254 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, int grid, uin
             ru = 0;
             float s0 = wave_sum(acc0);
             float s1 = m.unit == 2 ? wave_sum(acc1) : 0.f;
-            if (c.lane == 0) epilogue(c, p, unit, s0, s1);
-            unit += w.nw;
+            if (c.lane == 0) {
+              sums[finished][0] = s0;
+              sums[finished][1] = s1;
+            }
+            finished++;
             acc0 = 0.f;
             acc1 = 0.f;
           }
         }
       }
     }
+    // Epilogues of the finished units, outside the unrolled loop (one copy of the code).
+    if (c.lane == 0)
+      for (int k = 0; k < finished; k++) epilogue(c, p, unit + kStreamWaves * k, sums[k][0], sums[k][1], xres, first);
+    unit += kStreamWaves * finished;
   }
 }
 
 // ---------------------------------------------------------------------------------------------
-// stream waves: attention phase (src/cuda/Primitives.cuh:167-219, src/cpu/Cpu.cpp:97-109)
+// stream waves: attention (src/cuda/Primitives.cuh:167-219, src/cpu/Cpu.cpp:97-109)
+
+// Count one chunk partial of head h (after this wave's partial stores are complete); the
+// last chunk of the head to arrive combines all partials in chunk order,
+//   attn = sum_c o_c exp(m_c - M) / sum_c s_c exp(m_c - M),
+// and publishes attn_h. The wrapping increment leaves the counter at 0 for the next use.
+template <int P>
+__device__ __forceinline__ void attn_publish_and_combine(Ctx<P>& c, const AttnWork& w, int layer, int h, int nactive,
+                                                         float* scale) {
+  const StepArgs& a = c.a;
+  const int dim = a.dim;
+  __builtin_amdgcn_s_waitcnt(0);
+  unsigned old = 0;
+  if (c.lane == 0)
+    old = __builtin_amdgcn_atomic_inc32(a.head_count + h * 32, (unsigned)(nactive - 1), __ATOMIC_RELAXED, "agent");
+  old = __shfl(old, 0);
+  if ((int)old != nactive - 1) return;
+  const unsigned ep = c.epoch(ph_index(kAttn, layer));
+  const uint32_t hb = a.s_partial + (uint32_t)(h * w.nch) * (uint32_t)(dim + 2);
+  const uint32_t pstride = (uint32_t)(dim + 2);
+  float big = -INFINITY, denom = 0.f;
+  if (nactive <= 32 && dim <= 64) {
+    // one round of loads: (m_c, s_c) per lane, o_c[lane] for every chunk
+    int cl = c.lane < nactive ? c.lane : nactive - 1;
+    float mc = c.sload(hb + (uint32_t)cl * pstride);
+    float sc = c.sload(hb + (uint32_t)cl * pstride + 1u);
+    int il = c.lane < dim ? c.lane : dim - 1;
+    float part[32];
+#pragma unroll
+    for (int k = 0; k < 32; k++) {
+      int cc = k < nactive ? k : nactive - 1;
+      part[k] = c.sload(hb + (uint32_t)cc * pstride + 2u + (uint32_t)il);
+    }
+    big = wave_max(c.lane < nactive ? mc : -INFINITY);
+    float e = c.lane < nactive ? expf(mc - big) : 0.f;
+    denom = wave_sum(sc * e);
+    scale[c.lane] = e;
+    __builtin_amdgcn_wave_barrier();
+    float o = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; k++)
+      if (k < nactive) o += part[k] * scale[k];
+    if (c.lane < dim) c.tstore(a.t_attn + h * dim + c.lane, ep, cast<P>(o / denom));
+  } else {
+    for (int c0 = 0; c0 < nactive; c0 += 64) {
+      int cc = c0 + c.lane;
+      float mc = cc < nactive ? c.sload(hb + (uint32_t)cc * pstride) : -INFINITY;
+      big = fmaxf(big, mc);
+      if (cc < nactive) scale[cc] = mc;
+    }
+    big = wave_max(big);
+    for (int c0 = 0; c0 < nactive; c0 += 64) {
+      int cc = c0 + c.lane;
+      float sc = cc < nactive ? c.sload(hb + (uint32_t)cc * pstride + 1u) : 0.f;
+      float e = cc < nactive ? expf(scale[cc] - big) : 0.f;
+      if (cc < nactive) scale[cc] = e;
+      denom += sc * e;
+    }
+    denom = wave_sum(denom);
+    __builtin_amdgcn_wave_barrier();
+    for (int i = c.lane; i < dim; i += 64) {
+      float o = 0.f;
+      for (int c0 = 0; c0 < nactive; c0 += 16) {
+        float part[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+          int cc = c0 + k < nactive ? c0 + k : nactive - 1;
+          part[k] = c.sload(hb + (uint32_t)cc * pstride + 2u + (uint32_t)i);
+        }
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+          if (c0 + k < nactive) o += part[k] * scale[c0 + k];
+      }
+      c.tstore(a.t_attn + h * dim + i, ep, cast<P>(o / denom));
+    }
+  }
+}
+
+// Store element i of the current K and V rows of (layer, head h) into the ring.
+template <int P>
+__device__ __forceinline__ void ring_write(Ctx<P>& c, int layer, int h, int i, float kv, float vv) {
+  uint32_t idx =
+      ((uint32_t)(layer * c.a.heads + h) * (uint32_t)c.a.window + (uint32_t)c.slot) * (uint32_t)c.a.dim + (uint32_t)i;
+  if constexpr (P == kMixed) {
+    st2_coherent(c.kr, idx * 2u, float_to_half(kv));
+    st2_coherent(c.vr, idx * 2u, float_to_half(vv));
+  } else {
+    st4_coherent(c.kr, idx * 4u, kv);
+    st4_coherent(c.vr, idx * 4u, vv);
+  }
+}
+
+// Decode the 16-byte chunk of a K/V block into E floats.
+template <int P>
+__device__ __forceinline__ void kv_decode(uint4 u, float* v) {
+  if constexpr (P == kMixed) {
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      v[2 * e] = half_to_float((unsigned short)(w[e] & 0xffffu));
+      v[2 * e + 1] = half_to_float((unsigned short)(w[e] >> 16));
+    }
+  } else {
+    v[0] = __builtin_bit_cast(float, u.x);
+    v[1] = __builtin_bit_cast(float, u.y);
+    v[2] = __builtin_bit_cast(float, u.z);
+    v[3] = __builtin_bit_cast(float, u.w);
+  }
+}
+
+// Attention on the register-held K/V block (power-of-two head dim with E <= dim <= 64E,
+// E elements per 16-byte chunk). Lane l's j-th chunk holds row (l*E)/dim + j*(64E/dim),
+// columns (l*E)%dim .. +E-1; the dim/E lanes of a row reduce q.k with a butterfly and the
+// output columns reduce across rows the same way. Each wave polls the q, k, v elements of
+// its own head, so attention waits only on the QKV units of that head.
+template <int P>
+__device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ring)[kPF]) {
+  const StepArgs& a = c.a;
+  AttnWork w = attn_work<P>(a, c.grid, c.g, c.wave - 1);
+  constexpr int E = 16 / Traits<P>::kKvBytes;
+  const int dim = a.dim, chunk = a.chunk;
+  const int group = dim / E;
+  const int rows_per_load = 64 / group;
+  const int loads = (w.kchunks + 63) / 64;
+  const int col0 = (c.lane * E) % dim;
+  const int row_lane = (c.lane * E) / dim;
+  const int nactive = (c.valid + chunk - 1) / chunk;
+  const float div = sqrtf((float)dim);
+  const unsigned ep_qkv = c.epoch(ph_index(kQkv, p.layer));
+  float* scale = c.lds.stage[c.wave - 1];
+  for (int m = 0; m < w.items; m++) {
+    int it = w.wid + w.nw * m;
+    int h = it / w.nch, ch = it - h * w.nch;
+    if (ch >= nactive) continue;
+    if (m > 0) {
+      load_block<P>(c, c.kr, p.layer, h, ch, w.kchunks, ring);
+      load_block<P>(c, c.vr, p.layer, h, ch, w.kchunks, ring + kPF / 2);
+    }
+    // q, k, v of this lane's columns of head h (E each), polled from the tagged vectors.
+    float q[E], kc[E], vc[E];
+    {
+      uint4 pq[E / 2], pk[E / 2], pv[E / 2];
+      const uint32_t e0 = (uint32_t)(h * dim + col0);
+      unsigned long long start = wall_clock64();
+      while (true) {
+#pragma unroll
+        for (int k = 0; k < E / 2; k++) {
+          uint32_t off = (e0 + 2u * k) * 8u;
+          pq[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(c.tr, (int)(a.t_q * 8u + off), 0, kSc1));
+          pk[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(c.tr, (int)(a.t_k * 8u + off), 0, kSc1));
+          pv[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(c.tr, (int)(a.t_v * 8u + off), 0, kSc1));
+        }
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < E / 2; k++)
+          ok = ok && pq[k].y == ep_qkv && pq[k].w == ep_qkv && pk[k].y == ep_qkv && pk[k].w == ep_qkv &&
+               pv[k].y == ep_qkv && pv[k].w == ep_qkv;
+        if (__all(ok) || c.dead) break;
+        if (wall_clock64() - start > a.spin_limit) {
+          c.timeout();
+          break;
+        }
+        __builtin_amdgcn_s_sleep(kPollSleep);
+      }
+#pragma unroll
+      for (int k = 0; k < E / 2; k++) {
+        q[2 * k] = __builtin_bit_cast(float, pq[k].x);
+        q[2 * k + 1] = __builtin_bit_cast(float, pq[k].z);
+        kc[2 * k] = __builtin_bit_cast(float, pk[k].x);
+        kc[2 * k + 1] = __builtin_bit_cast(float, pk[k].z);
+        vc[2 * k] = __builtin_bit_cast(float, pv[k].x);
+        vc[2 * k + 1] = __builtin_bit_cast(float, pv[k].z);
+      }
+    }
+    const int row0 = ch * chunk;
+    const bool owns_slot = c.slot >= row0 && c.slot < row0 + chunk;
+    if (owns_slot && c.lane < group) {
+#pragma unroll
+      for (int e = 0; e < E; e++) ring_write(c, p.layer, h, col0 + e, kc[e], vc[e]);
+    }
+    float logit[kPF / 2];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kPF / 2; j++) {
+      int row = row_lane + j * rows_per_load;
+      bool live = j < loads && (c.lane + 64 * j) < w.kchunks && row < chunk && row0 + row < c.valid;
+      bool cur = row0 + row == c.slot;
+      float k[E];
+      kv_decode<P>(ring[j], k);
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; e++) dot += q[e] * (cur ? kc[e] : k[e]);
+      for (int o = group >> 1; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
+      logit[j] = live ? dot / div : -INFINITY;
+      mx = fmaxf(mx, logit[j]);
+    }
+    mx = wave_max(mx);
+    float psum = 0.f;
+    float out[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) out[e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPF / 2; j++) {
+      float pr = logit[j] == -INFINITY ? 0.f : expf(logit[j] - mx);
+      psum += pr;
+      int row = row_lane + j * rows_per_load;
+      bool cur = row0 + row == c.slot;
+      float v[E];
+      kv_decode<P>(ring[kPF / 2 + j], v);
+#pragma unroll
+      for (int e = 0; e < E; e++) out[e] += pr * (cur ? vc[e] : v[e]);
+    }
+    float total = wave_sum((c.lane & (group - 1)) == 0 ? psum : 0.f);
+#pragma unroll
+    for (int e = 0; e < E; e++)
+      for (int o = 32; o >= group; o >>= 1) out[e] += __shfl_xor(out[e], o);
+    uint32_t pbase = a.s_partial + ((uint32_t)(h * w.nch + ch)) * (uint32_t)(dim + 2);
+    if (c.lane < group) {
+#pragma unroll
+      for (int e = 0; e < E; e++) c.sstore(pbase + 2 + col0 + e, out[e]);
+    }
+    if (c.lane == 0) {
+      c.sstore(pbase, mx);
+      c.sstore(pbase + 1, total);
+    }
+    attn_publish_and_combine(c, w, p.layer, h, nactive, scale);
+    __builtin_amdgcn_wave_barrier();
+  }
+}
 
 // Write a prefetched K or V block (register ring half) into this wave's LDS stage as
 // [chunk rows][dim + 4] floats. Row/column of each element advance incrementally.
@@ -299,19 +705,7 @@ __device__ __forceinline__ void block_to_lds(Ctx<P>& c, const uint4* part, int k
   for (int j = 0; j < kPF / 2; j++) {
     if (c.lane + 64 * j < kchunks) {
       float v[kPer];
-      if constexpr (P == kMixed) {
-        uint32_t u[4] = {part[j].x, part[j].y, part[j].z, part[j].w};
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          v[2 * e] = half_to_float((unsigned short)(u[e] & 0xffffu));
-          v[2 * e + 1] = half_to_float((unsigned short)(u[e] >> 16));
-        }
-      } else {
-        v[0] = __builtin_bit_cast(float, part[j].x);
-        v[1] = __builtin_bit_cast(float, part[j].y);
-        v[2] = __builtin_bit_cast(float, part[j].z);
-        v[3] = __builtin_bit_cast(float, part[j].w);
-      }
+      kv_decode<P>(part[j], v);
       int r = row, cc = col;
 #pragma unroll
       for (int e = 0; e < kPer; e++) {
@@ -331,19 +725,12 @@ __device__ __forceinline__ void block_to_lds(Ctx<P>& c, const uint4* part, int k
   }
 }
 
-// Load the K or V block of item (h, ch) directly (items beyond the first of a wave).
+// General head dims: K/V block staged through LDS, q/k/v of the step staged by the control
+// wave (lds.qkv).
 template <int P>
-__device__ __forceinline__ void load_block(Ctx<P>& c, __amdgpu_buffer_rsrc_t r, int layer, int h, int ch,
-                                  int kchunks, uint4* part) {
-#pragma unroll
-  for (int j = 0; j < kPF / 2; j++)
-    part[j] = ld16(r, attn_chunk_offset<P>(c.a, layer, h, ch, c.lane + 64 * j, kchunks));
-}
-
-template <int P>
-__device__ __forceinline__ void compute_attn(Ctx<P>& c, Phase p, int grid, uint4 (&ring)[kPF]) {
+__device__ __forceinline__ void compute_attn_lds(Ctx<P>& c, Phase p, uint4 (&ring)[kPF]) {
   const StepArgs& a = c.a;
-  AttnWork w = attn_work<P>(a, grid, c.g, c.wave - 1);
+  AttnWork w = attn_work<P>(a, c.grid, c.g, c.wave - 1);
   const int dim = a.dim, stride = dim + 4, chunk = a.chunk;
   float* stage = c.lds.stage[c.wave - 1];
   float* probs = c.lds.probs[c.wave - 1];
@@ -351,7 +738,7 @@ __device__ __forceinline__ void compute_attn(Ctx<P>& c, Phase p, int grid, uint4
   const float* k_cur = c.lds.qkv + kMaxDim;
   const float* v_cur = c.lds.qkv + 2 * kMaxDim;
   const int nactive = (c.valid + chunk - 1) / chunk;
-  const float inv_scale_div = sqrtf((float)dim);
+  const float div = sqrtf((float)dim);
   for (int m = 0; m < w.items; m++) {
     int it = w.wid + w.nw * m;
     int h = it / w.nch, ch = it - h * w.nch;
@@ -362,84 +749,60 @@ __device__ __forceinline__ void compute_attn(Ctx<P>& c, Phase p, int grid, uint4
     }
     int row0 = ch * chunk;
     int rows = c.valid - row0 < chunk ? c.valid - row0 : chunk;  // valid slots are [0, valid)
-    // K block -> LDS, then patch in the slot written this step
-    block_to_lds<P>(c, ring, w.kchunks, stage);
     int cur = c.slot - row0;
+    if (cur >= 0 && cur < chunk)
+      for (int i = c.lane; i < dim; i += 64) ring_write(c, p.layer, h, i, k_cur[h * dim + i], v_cur[h * dim + i]);
+    block_to_lds<P>(c, ring, w.kchunks, stage);
     if (cur >= 0 && cur < chunk)
       for (int i = c.lane; i < dim; i += 64) stage[cur * stride + i] = k_cur[h * dim + i];
     __builtin_amdgcn_wave_barrier();
     float logit = -INFINITY;
     if (c.lane < rows) {
-      const float* kr = stage + c.lane * stride;
+      const float* krow = stage + c.lane * stride;
       const float* q = q_all + h * dim;
       float dot = 0.f;
-      for (int i = 0; i < dim; i++) dot += q[i] * kr[i];
-      logit = dot / inv_scale_div;
+      for (int i = 0; i < dim; i++) dot += q[i] * krow[i];
+      logit = dot / div;
     }
     float mx = wave_max(logit);
     float pr = c.lane < rows ? expf(logit - mx) : 0.f;
     float total = wave_sum(pr);
-    if (c.lane < 64) probs[c.lane] = pr;
+    probs[c.lane] = pr;
     __builtin_amdgcn_wave_barrier();
-    // V block -> LDS (overwrites K)
     block_to_lds<P>(c, ring + kPF / 2, w.kchunks, stage);
     if (cur >= 0 && cur < chunk)
       for (int i = c.lane; i < dim; i += 64) stage[cur * stride + i] = v_cur[h * dim + i];
     __builtin_amdgcn_wave_barrier();
-    uint32_t pbase = ((uint32_t)(h * w.nch + ch)) * (uint32_t)(dim + 2);
+    uint32_t pbase = a.s_partial + ((uint32_t)(h * w.nch + ch)) * (uint32_t)(dim + 2);
     for (int i = c.lane; i < dim; i += 64) {
       float o = 0.f;
       for (int j = 0; j < rows; j++) o += probs[j] * stage[j * stride + i];
-      c.sstore(a.s_partial + pbase + 2 + i, o);
+      c.sstore(pbase + 2 + i, o);
     }
     if (c.lane == 0) {
-      c.sstore(a.s_partial + pbase, mx);
-      c.sstore(a.s_partial + pbase + 1, total);
+      c.sstore(pbase, mx);
+      c.sstore(pbase + 1, total);
     }
-    // Publish the partial, then count it; the last chunk of the head combines.
-    __builtin_amdgcn_s_waitcnt(0);
-    unsigned old = 0;
-    if (c.lane == 0)
-      old = __hip_atomic_fetch_add(a.head_count + h * 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __shfl(old, 0);
-    if ((int)old == nactive - 1) {
-      float big = -INFINITY;
-      for (int cc = 0; cc < nactive; cc++)
-        big = fmaxf(big, c.sload(a.s_partial + (uint32_t)(h * w.nch + cc) * (uint32_t)(dim + 2)));
-      float denom = 0.f;
-      for (int cc = 0; cc < nactive; cc++) {
-        uint32_t b = (uint32_t)(h * w.nch + cc) * (uint32_t)(dim + 2);
-        denom += c.sload(a.s_partial + b + 1) * expf(c.sload(a.s_partial + b) - big);
-      }
-      for (int i = c.lane; i < dim; i += 64) {
-        float o = 0.f;
-        for (int cc = 0; cc < nactive; cc++) {
-          uint32_t b = (uint32_t)(h * w.nch + cc) * (uint32_t)(dim + 2);
-          o += c.sload(a.s_partial + b + 2 + i) * expf(c.sload(a.s_partial + b) - big);
-        }
-        c.sstore(a.s_attn + h * dim + i, cast<P>(o / denom));
-      }
-      if (c.lane == 0)
-        __hip_atomic_store(a.head_count + h * 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    attn_publish_and_combine(c, w, p.layer, h, nactive, stage);
     __builtin_amdgcn_wave_barrier();
   }
 }
 
 // Final phase (workgroup 0, control wave): score = W_score . norm(x), not cast; position++.
 template <int P>
-__device__ __forceinline__ void compute_final(Ctx<P>& c) {
+__device__ __forceinline__ void compute_final(Ctx<P>& c, const float* xs_buf) {
   const StepArgs& a = c.a;
-  const int chunks = a.width_p / Traits<P>::kEpc;
-  float acc = 0.f;
-  for (int s = 0; s * 64 < chunks; s++) {
-    int chunk = s * 64 + c.lane;
-    bool live = chunk < chunks;
-    int cc = live ? chunk : chunks - 1;
-    uint4 wv = ld16(c.wr, a.w_score + (uint32_t)cc * 16u);
-    float d = chunk_dot<P>(wv, c.lds.xs + cc * Traits<P>::kEpc);
-    acc += live ? d : 0.f;
+  const int slabs = a.width_p * Traits<P>::kWBytes / 1024;  // <= 4
+  uint4 wv[kMaxDim * 4 / 1024];
+#pragma unroll
+  for (int s = 0; s < kMaxDim * 4 / 1024; s++) {
+    int sc = s < slabs ? s : slabs - 1;
+    wv[s] = ld16(c.wr, a.w_score + (uint32_t)sc * 1024u + (uint32_t)c.lane * 16u);
   }
+  float acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < kMaxDim * 4 / 1024; s++)
+    if (s < slabs) acc += chunk_dot<P>(wv[s], xs_buf + (s * 64 + c.lane) * Traits<P>::kEpc);
   float score = wave_sum(acc);
   if (c.lane == 0) {
     c.sstore(a.s_score, score);
@@ -447,42 +810,14 @@ __device__ __forceinline__ void compute_final(Ctx<P>& c) {
   }
 }
 
-template <int P>
-__device__ __forceinline__ void compute(Ctx<P>& c, Phase p, int grid, uint4 (&ring)[kPF]) {
-  if (p.kind == kAttn) compute_attn(c, p, grid, ring);
-  else if (p.kind != kFinal) compute_matvec(c, p, grid, ring);
-}
-
-// ---------------------------------------------------------------------------------------------
-// grid barrier: per-workgroup flags, written through to the device coherence point
-
-__device__ __forceinline__ void grid_arrive(const StepArgs& a, int g, unsigned epoch) {
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete
-  __builtin_amdgcn_s_barrier();
-  if (threadIdx.x == 0)
-    __hip_atomic_store(a.flags + g * kFlagStride, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Control wave only. Returns false on timeout (sets the sticky error bit).
-__device__ __forceinline__ bool grid_wait(const StepArgs& a, int grid, unsigned epoch) {
-  const int lane = lane_id();
-  unsigned long long start = wall_clock64();
-  while (true) {
-    bool ok = true;
-#pragma unroll
-    for (int k = 0; k < kMaxGrid / 64; k++) {
-      int i = lane + 64 * k;
-      if (k * 64 < grid) {
-        int j = i < grid ? i : grid - 1;
-        unsigned f = __hip_atomic_load(a.flags + j * kFlagStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ok = ok && (int)(f - epoch) >= 0;
-      }
-    }
-    if (__all(ok)) return true;
-    if (wall_clock64() - start > a.spin_limit) {
-      if (lane == 0) __hip_atomic_fetch_or(a.error, kErrBarrierTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return false;
-    }
+// A = 1: register attention path; A = 0: LDS path (general head dims).
+template <int P, int A>
+__device__ __forceinline__ void compute(Ctx<P>& c, Phase p, int buf, uint4 (&ring)[kPF]) {
+  if (p.kind == kAttn) {
+    if constexpr (A == 1) compute_attn_regs(c, p, ring);
+    else compute_attn_lds(c, p, ring);
+  } else if (p.kind != kFinal) {
+    compute_matvec(c, p, c.lds.xs[buf], c.lds.xres[buf], ring);
   }
 }
 
@@ -494,111 +829,135 @@ __device__ __forceinline__ void lds_barrier() {
 // ---------------------------------------------------------------------------------------------
 // kernels
 
-// One phase per launch (staged and graph backends).
-template <int P>
+// One phase per launch (staged and graph backends). The FINAL launch advances the epoch.
+template <int P, int A>
 __global__ __launch_bounds__(kThreads) void phase_kernel(const StepArgs* __restrict__ ap, int ph) {
   const StepArgs& a = *ap;
   __shared__ LdsAll lds;
-  Ctx<P> c(a, lds, (int)blockIdx.x);
-  c.set_position(load_position(a));
+  Ctx<P> c(a, lds, (int)blockIdx.x, (int)gridDim.x);
   Phase p = phase_of(a, ph);
   if (p.kind == kFinal && blockIdx.x != 0) return;
+  c.base = load_epoch(a);
+  c.set_position(load_position(a));
   uint4 ring[kPF];
-  if (c.wave == 0) stage_inputs(c, p);
-  else prefetch(c, p, (int)gridDim.x, ring);
+  for (int i = threadIdx.x; i < a.dim / 2; i += kThreads) c.lds.rope[i] = a.rope_freq[i];
+  if (c.wave == 0) stage_inputs<P, A>(c, p, 0);
+  else prefetch(c, p, ring);
   lds_barrier();
   if (p.kind == kFinal) {
-    if (c.wave == 0) compute_final(c);
+    if (c.wave == 0) {
+      compute_final(c, c.lds.xs[0]);
+      if (c.lane == 0)
+        __hip_atomic_store(a.epoch, c.base + (unsigned)ph_final(a) + 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     return;
   }
-  if (c.wave != 0) compute(c, p, (int)gridDim.x, ring);
+  if (c.wave != 0) compute<P, A>(c, p, 0, ring);
 }
 
-// One forward over the device-held state. Used by the fused, persistent and trace kernels.
-// The epoch argument counts barriers; returns the next epoch.
-template <int P>
-__device__ __forceinline__ unsigned forward(Ctx<P>& c, int grid, unsigned epoch, uint4 (&ring)[kPF],
-                                   bool barrier_after_final) {
+// One forward over the device-held state with the context's position and epoch base.
+template <int P, int A>
+__device__ __forceinline__ void forward(Ctx<P>& c, uint4 (&ring)[kPF]) {
   const StepArgs& a = c.a;
-  const int nph = 5 * a.layers + 2;
-  if (c.wave == 0) stage_inputs(c, phase_of(a, 0));
-  else prefetch(c, phase_of(a, 0), grid, ring);
-  lds_barrier();
-  for (int ph = 0; ph + 1 < nph; ph++) {
-    Phase p = phase_of(a, ph);
-    if (c.wave != 0) compute(c, p, grid, ring);
-    grid_arrive(a, c.g, ++epoch);
-    Phase next = phase_of(a, ph + 1);
-    if (next.kind == kFinal && c.g != 0) {
-      if (barrier_after_final) {
-        // Nothing to publish: arrive at once for the post-FINAL barrier and wait for
-        // workgroup 0 to finish the score and the position update.
-        grid_arrive(a, c.g, ++epoch);
-        if (c.wave == 0) grid_wait(a, grid, epoch);
-        __builtin_amdgcn_s_barrier();
-      }
-      return epoch;
-    }
-    if (c.wave == 0) {
-      grid_wait(a, grid, epoch);
-      stage_inputs(c, next);
-    } else {
-      prefetch(c, next, grid, ring);
-    }
+  const int nph = ph_final(a) + 1;
+  const bool stamp = a.stamps && c.g == 0 && threadIdx.x == 0;
+  if (threadIdx.x == 0) {
+    c.lds.done[0] = 0;
+    c.lds.done[1] = 0;
+  }
+  for (int i = threadIdx.x; i < a.dim / 2; i += kThreads) c.lds.rope[i] = a.rope_freq[i];
+  if (c.wave == 0) stage_inputs<P, A>(c, phase_of(a, 0), 0);
+  else prefetch(c, phase_of(a, 0), ring);
+  // Optional stamps (workgroup 0): per phase [start, first stream wave done, staging
+  // started, staging done]; the end of the step follows the last phase.
+  const bool stamp_wave = a.stamps && c.g == 0 && c.lane == 0;
+  for (int ph = 0; ph < nph; ph++) {
     lds_barrier();
+    if (stamp) a.stamps[4 * ph] = wall_clock64();
+    Phase p = phase_of(a, ph);
+    if (p.kind == kFinal) {
+      if (c.g == 0 && c.wave == 0) compute_final(c, c.lds.xs[ph & 1]);
+      if (stamp) a.stamps[4 * nph] = wall_clock64();
+      break;
+    }
+    if (c.wave != 0) {
+      compute<P, A>(c, p, ph & 1, ring);
+      if (stamp_wave && c.wave == 1) a.stamps[4 * ph + 1] = wall_clock64();
+      prefetch(c, phase_of(a, ph + 1), ring);
+      if (c.lane == 0) __hip_atomic_fetch_add(&c.lds.done[ph & 1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else {
+      // Start polling for the next phase's inputs only once this workgroup's own part of
+      // the current phase is done: the producers elsewhere finish at about the same time,
+      // and polling earlier would only add memory traffic.
+      while (__hip_atomic_load(&c.lds.done[ph & 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)kStreamWaves)
+        __builtin_amdgcn_s_sleep(1);
+      if (c.lane == 0) __hip_atomic_store(&c.lds.done[ph & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (stamp) a.stamps[4 * ph + 2] = wall_clock64();
+      stage_inputs<P, A>(c, phase_of(a, ph + 1), (ph + 1) & 1);
+      if (stamp) a.stamps[4 * ph + 3] = wall_clock64();
+    }
   }
-  // FINAL (workgroup 0 only)
-  if (c.wave == 0) compute_final(c);
-  if (barrier_after_final) {
-    grid_arrive(a, c.g, ++epoch);
-    if (c.wave == 0) grid_wait(a, grid, epoch);
-    __builtin_amdgcn_s_barrier();
-  }
-  return epoch;
 }
 
-template <int P>
-__global__ __launch_bounds__(kThreads) void fused_kernel(const StepArgs* __restrict__ ap) {
+// One step per launch (fused backend). `event` overrides the INPUT source when not null.
+template <int P, int A>
+__global__ __launch_bounds__(kThreads) void fused_kernel(const StepArgs* __restrict__ ap, const float* event) {
   const StepArgs& a = *ap;
   __shared__ LdsAll lds;
-  Ctx<P> c(a, lds, (int)blockIdx.x);
+  Ctx<P> c(a, lds, (int)blockIdx.x, (int)gridDim.x);
+  if (event) c.input = event;
+  c.base = load_epoch(a);
   c.set_position(load_position(a));
-  unsigned epoch0 = __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   uint4 ring[kPF];
-  unsigned end = forward(c, (int)gridDim.x, epoch0, ring, false);
+  forward<P, A>(c, ring);
   if (blockIdx.x == 0 && threadIdx.x == 0)
-    __hip_atomic_store(a.epoch, end, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.epoch, c.base + (unsigned)ph_final(a) + 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Device-only timing loop over a preloaded trace: per-event wall-clock stamps.
-template <int P>
-__global__ __launch_bounds__(kThreads) void trace_kernel(const StepArgs* __restrict__ ap, const float* events,
-                                                         int count, unsigned long long* stamps) {
+// Device-only loop over a preloaded trace (the reference's trace_kernel): `count` steps in
+// one cooperative launch, with a wall-clock stamp per step from workgroup 0. Workgroup 0
+// publishes a step-done word after each FINAL; every workgroup waits for it before the
+// next step writes x.
+template <int P, int A>
+__global__ __launch_bounds__(kThreads) void trace_kernel(const StepArgs* __restrict__ ap, const float* events, int count,
+                                                         unsigned long long* stamps) {
   const StepArgs& a = *ap;
   __shared__ LdsAll lds;
-  Ctx<P> c(a, lds, (int)blockIdx.x);
-  unsigned epoch = __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  Ctx<P> c(a, lds, (int)blockIdx.x, (int)gridDim.x);
+  const unsigned base0 = load_epoch(a);
+  const unsigned long long t0 = load_position(a);
+  const unsigned per_step = (unsigned)ph_final(a) + 2u;  // phases + the step-done word
   uint4 ring[kPF];
   for (int e = 0; e < count; e++) {
     if (blockIdx.x == 0 && threadIdx.x == 0) stamps[e] = wall_clock64();
-    c.set_position(load_position(a));
+    c.base = base0 + (unsigned)e * per_step;
+    c.set_position(t0 + (unsigned long long)e);
     c.input = events + (size_t)e * a.features_p;
-    epoch = forward(c, (int)gridDim.x, epoch, ring, true);
+    if (e > 0 && c.wave == 0) {
+      float done[2];
+      poll_pieces<P, 1>(c, a.t_done, 1, 0, 1, c.base - 1u, done);
+    }
+    forward<P, A>(c, ring);
+    if (c.g == 0 && threadIdx.x == 0) c.tstore(a.t_done, c.base + per_step - 1u, 0.f);
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     stamps[count] = wall_clock64();
-    __hip_atomic_store(a.epoch, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.epoch, base0 + (unsigned)count * per_step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 // Zero K/V, hidden state, attention counters and the position (src/cuda/Primitives.cuh:280-292).
+// Tagged vectors keep their tags: epochs only grow.
 __global__ void reset_kernel(const StepArgs* __restrict__ ap) {
   const StepArgs& a = *ap;
   size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   size_t stride = (size_t)gridDim.x * blockDim.x;
   uint32_t* k = reinterpret_cast<uint32_t*>(a.keys);
   uint32_t* v = reinterpret_cast<uint32_t*>(a.values);
-  for (size_t i = tid; i < a.cache_bytes / 4; i += stride) { k[i] = 0; v[i] = 0; }
+  for (size_t i = tid; i < a.cache_bytes / 4; i += stride) {
+    k[i] = 0;
+    v[i] = 0;
+  }
   for (size_t i = tid; i < (size_t)a.layers * a.width; i += stride) a.scratch[a.s_hidden + i] = 0.f;
   for (size_t i = tid; i < (size_t)a.heads * 32; i += stride) a.head_count[i] = 0;
   if (tid == 0) *a.position = 0;

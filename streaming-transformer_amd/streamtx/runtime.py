@@ -97,12 +97,16 @@ def library(path: os.PathLike | None = None) -> ctypes.CDLL:
     lib.st_runtime_stop.argtypes = [P]
     lib.st_runtime_snapshot.argtypes = [P, ctypes.POINTER(ctypes.c_uint64), F, F, F]
     lib.st_runtime_device_trace.argtypes = [P, F, ctypes.c_size_t, D, D]
+    lib.st_runtime_device_run.argtypes = [P, F, ctypes.c_size_t, ctypes.c_int32, D, D]
+    lib.st_runtime_phase_times.argtypes = [P, F, D, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_runtime_info_json.argtypes = [P, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_probe_json.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_last_error.argtypes = []
     lib.st_last_error.restype = ctypes.c_char_p
     for name in ('st_runtime_create', 'st_runtime_step', 'st_runtime_reset', 'st_runtime_stop',
-                 'st_runtime_snapshot', 'st_runtime_device_trace', 'st_runtime_info_json', 'st_probe_json'):
+                 'st_runtime_snapshot', 'st_runtime_device_trace', 'st_runtime_device_run', 'st_runtime_phase_times',
+                 'st_runtime_info_json',
+                 'st_probe_json'):
         getattr(lib, name).restype = ctypes.c_int
     _lib = lib
     return lib
@@ -223,6 +227,30 @@ class Runtime:
         _check(library().st_runtime_device_trace(self._handle(), _fptr(x), x.shape[0], ctypes.byref(mean),
                                                  per.ctypes.data_as(ctypes.POINTER(ctypes.c_double))))
         return float(mean.value), per
+
+    def device_run(self, inputs, reset: bool = False):
+        """Per-launch device timing (extension): one step per launch, HIP events on the
+        runtime's stream; continues the current state unless reset. (mean us, per-event us)."""
+        x = np.ascontiguousarray(inputs, dtype=np.float32).reshape(-1, self.config.features)
+        per = np.empty(x.shape[0], dtype=np.float64)
+        mean = ctypes.c_double(0)
+        _check(library().st_runtime_device_run(self._handle(), _fptr(x), x.shape[0], int(reset),
+                                               ctypes.byref(mean),
+                                               per.ctypes.data_as(ctypes.POINTER(ctypes.c_double))))
+        return float(mean.value), per
+
+    def phase_times(self, event):
+        """One fused step with stamps (extension): (array [phases, 4] of microseconds since
+        the step started: phase start, first stream wave done, staging start, staging done;
+        step end)."""
+        x = np.ascontiguousarray(event, dtype=np.float32)
+        n = 4 * (5 * self.config.layers + 2) + 1
+        out = np.empty(n, dtype=np.float64)
+        count = ctypes.c_size_t(0)
+        _check(library().st_runtime_phase_times(self._handle(), _fptr(x),
+                                                out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), n,
+                                                ctypes.byref(count)))
+        return out[:-1].reshape(-1, 4), float(out[-1])
 
     def info(self) -> dict:
         return _json(library().st_runtime_info_json, self._handle())
