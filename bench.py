@@ -81,6 +81,30 @@ def cpu_baseline(c: ModelConfig, weights, mixed, events, fill: int, sample: int)
     return out, threads_all
 
 
+def copy_calibration(mib: int) -> None:
+    """A plain copy kernel of known size: each launch reads and writes `mib` MiB. Profiling
+    it with the FETCH_SIZE / WRITE_SIZE counters gives the factor between counter readings
+    and HBM bytes on this device."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.empty(n, dtype=torch.float32, device='cuda').uniform_()
+    dst = torch.empty_like(src)
+    for _ in range(8):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({'copy_calibration_bytes_per_launch': n * 4, 'launches': 8}), flush=True)
+
+
+def traffic_per_launch(path: Path):
+    """HBM bytes per launch from a committed counter summary (line `hbm_bytes_per_launch: N`)."""
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith('hbm_bytes_per_launch:'):
+            return int(float(line.split(':', 1)[1]))
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument('--gpus', type=int, default=1)
@@ -91,7 +115,12 @@ def main():
     ap.add_argument('--backend', choices=['fused', 'graph', 'cuda'], default='fused')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--quick', action='store_true', help='skip the secondary measurements')
+    ap.add_argument('--copy-calibration', type=int, metavar='MIB', default=0,
+                    help='only run 8 plain device copies of MIB MiB (reference kernel for HBM counters)')
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1:
         print(f'bench.py measures one GPU: the streaming step is a single ordered stream and this '
               f'build does not shard it (requested --gpus {args.gpus}).', file=sys.stderr)
@@ -142,10 +171,8 @@ def main():
                 'algorithmic_bytes_per_step': bytes_step,
                 'roofline_us_per_step': bytes_step / (HBM_PEAK_GBS * 1e9) * 1e6,
                 'kernel': 'fused_kernel' if backend == Backend.FUSED else 'phase_kernel sequence'}
-    traffic_file = ROOT / 'profiles' / f'traffic_{args.backend}_{args.config}_{args.precision}.json'
-    if traffic_file.exists():
-        t = json.loads(traffic_file.read_text())
-        roofline['traffic'] = t.get('hbm_bytes_per_launch')
+    roofline['traffic'] = traffic_per_launch(
+        ROOT / 'profiles' / f'traffic_{args.backend}_kernel_{args.config}_{args.precision}.md')
     roofline['frac_p50'] = round(bytes_step / (p50 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
     extra['mall_resident'] = bytes_step < 256e6
 

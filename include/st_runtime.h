@@ -132,11 +132,14 @@ int st_runtime_device_run(st_runtime* runtime, const float* inputs, size_t count
                           double* us_per_event, double* per_event_us);
 
 /* Extension (no counterpart in the reference): one FUSED step on `input` (advancing the
- * stream like st_runtime_step) with wall-clock stamps from workgroup 0. For each of the
- * 5*layers+2 phases writes four times in microseconds since the step started: phase start,
- * first stream wave done with the phase, control wave starts staging the next phase's
- * inputs, staging done (0 where not recorded); then the end of the step. Writes
- * min(cap, 4*phases+1) values and the full count. */
+ * stream like st_runtime_step) with wall-clock stamps, for profiling. For each of the
+ * 5*layers+2 phases and each of the `blocks` workgroups (phase-major) writes 8 times in
+ * microseconds since workgroup 0 started the step: phase start, stream wave 1 done with the
+ * phase, all stream waves done (staging of the next phase's inputs starts), staging done,
+ * then three progress marks of stream wave 1 (matvec: work set up, first slab consumed, last
+ * slab consumed; attention: inputs polled, partial stored, combine done), and the time stream
+ * wave 1 finished issuing the next phase's prefetch; 0 where not recorded. The end of the step follows. Writes min(cap, 8*phases*blocks+1)
+ * values and the full count; with cap 0 only the count is written and no step runs. */
 int st_runtime_phase_times(st_runtime* runtime, const float* input, double* us, size_t cap,
                            size_t* count);
 

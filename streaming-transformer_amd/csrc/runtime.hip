@@ -683,15 +683,15 @@ double Runtime::device_run(const float* inputs, size_t count, bool reset_first, 
   return total_ms * 1000.0 / count;
 }
 
-// One fused step with wall-clock stamps from workgroup 0. For each phase writes four
-// times in microseconds since the step started: phase start (all waves released), first
-// stream wave done with the phase, control wave starts staging the next phase's inputs,
-// staging done (0 where not recorded); then the end of the step.
+// One fused step with wall-clock stamps. For each phase and workgroup writes kStamps times
+// in microseconds since workgroup 0 started the step (slots as in stamp()); 0 where not
+// recorded; then the end of the step.
 size_t Runtime::phase_times(const float* input, double* us, size_t cap) {
   if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
   if (opt_.backend != ST_BACKEND_FUSED) throw Error(ST_ERR_INVALID, "Phase stamps require the fused backend");
   const int nph = 5 * c_.layers + 2;
-  const size_t n = (size_t)4 * nph + 1;
+  const size_t n = (size_t)kStamps * nph * grid_ + 1;
+  if (cap == 0) return n;  // size query: no step
   DeviceBuffer stamps, args;
   stamps.alloc(n * 8);
   HIP_CHECK(hipMemset(stamps.ptr, 0, n * 8));

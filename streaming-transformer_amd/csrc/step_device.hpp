@@ -34,6 +34,7 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kStreamWaves = kWaves - 1;
 constexpr int kPF = 16;            // register ring depth (slabs) per stream wave
+constexpr int kStamps = 8;         // wall-clock stamps per phase and workgroup (profiling only)
 constexpr int kMaxGrid = 1024;     // largest grid accepted
 constexpr int kMaxLayers = 16;
 constexpr int kXs = 4096 + 64;     // LDS activation vector capacity (floats)

@@ -18,17 +18,22 @@
 
 #include "step_device.hpp"
 
+#ifndef STAMD_ORDER
+#define STAMD_ORDER 1
+#endif
+
 namespace stamd {
 
 struct LdsAll {
   float xs[2][kXs];                      // phase input vector, double buffered by phase parity
-  float xres[2][kMaxDim];                // own rows of x for the OUT/DOWN residuals
+  float xres[2][kMaxDim];                // x before this layer (OUT residual) and after OUT (DOWN residual)
   float qkv[3 * kMaxDim];                // attention LDS path: q, k, v of the step
   float stage[kStreamWaves][kAttnLds];   // attention LDS path: per-wave K/V staging; combine scale
   float probs[kStreamWaves][64];
   float sums[kStreamWaves][kPF][2];      // row sums of units finished in the current ring pass
   float rope[kMaxDim / 2];               // RoPE inverse frequencies
   unsigned done[2];                      // stream waves finished with the phase of this parity
+  unsigned staged;                       // phases whose successor's inputs are staged
 };
 
 template <int P>
@@ -84,6 +89,22 @@ __device__ __forceinline__ int ph_index(int kind, int layer) { return kind == kI
 __device__ __forceinline__ int ph_final(const StepArgs& a) { return 1 + 5 * a.layers; }
 // Phase that last wrote x before `layer`'s QKV phase.
 __device__ __forceinline__ int ph_x_before(int layer) { return layer == 0 ? 0 : ph_index(kDown, layer - 1); }
+
+// Profiling stamp k of phase p for this workgroup (lane 0 of the calling wave), when the
+// launch carries a stamp buffer. Slots: 0 phase start, 1 stream wave 1 done, 2 all stream
+// waves done, 3 next phase's inputs staged, 4-6 progress of stream wave 1 within the phase,
+// 7 stream wave 1 has issued the next phase's prefetch.
+__device__ __forceinline__ void put_stamp(unsigned long long* base, size_t index) {
+  // A global (not flat) store: it counts only against vmcnt, so LDS waits never wait for it.
+  typedef __attribute__((address_space(1))) unsigned long long gu64;
+  ((gu64*)base)[index] = wall_clock64();
+}
+
+template <int P>
+__device__ __forceinline__ void stamp(Ctx<P>& c, Phase p, int k) {
+  if (c.a.stamps && c.lane == 0)
+    put_stamp(c.a.stamps, (size_t)kStamps * ((size_t)ph_index(p.kind, p.layer) * (size_t)c.grid + (size_t)c.g) + (size_t)k);
+}
 
 // ---------------------------------------------------------------------------------------------
 // polling tagged vectors
@@ -181,28 +202,46 @@ __device__ __forceinline__ void poll_range(Ctx<P>& c, uint32_t tv, int first, in
 
 // RMSNorm in place over v[0 .. width) (src/cuda/Primitives.cuh:122-135):
 // s = 1/sqrt(sum(v^2)/d + eps), v = cast(v * s * w).
+constexpr int kNormK = kMaxDim / 64;  // norm weights per lane
+
+// Issue the loads of a norm weight vector (lane i holds elements i, i + 64, ...).
 template <int P>
-__device__ __forceinline__ void norm_in_lds(Ctx<P>& c, float* v, uint32_t w_off) {
+__device__ __forceinline__ void load_norm(Ctx<P>& c, uint32_t w_off, float (&w)[kNormK]) {
   const int d = c.a.width;
-  constexpr int K = kMaxDim / 64;
-  float w[K];
 #pragma unroll
-  for (int k = 0; k < K; k++) {
+  for (int k = 0; k < kNormK; k++) {
     int i = c.lane + 64 * k;
     w[k] = load_weight_scalar<P>(c.wr, w_off, i < d ? i : d - 1);
   }
+}
+
+// RMSNorm in place over v[0 .. width) (src/cuda/Primitives.cuh:122-135):
+// s = 1/sqrt(sum(v^2)/d + eps), v = cast(v * s * w).
+template <int P>
+__device__ __forceinline__ void norm_in_lds(Ctx<P>& c, float* v, const float (&w)[kNormK]) {
+  const int d = c.a.width;
   float sum = 0.f;
 #pragma unroll
-  for (int k = 0; k < K; k++) {
+  for (int k = 0; k < kNormK; k++) {
     int i = c.lane + 64 * k;
     if (i < d) sum += v[i] * v[i];
   }
   sum = wave_sum(sum);
   const float scale = 1.0f / sqrtf(sum / (float)d + c.a.epsilon);
 #pragma unroll
-  for (int k = 0; k < K; k++) {
+  for (int k = 0; k < kNormK; k++) {
     int i = c.lane + 64 * k;
     if (i < d) v[i] = cast<P>(v[i] * scale * w[k]);
+  }
+}
+
+// Copy v[0 .. width) to dst (the raw x kept for a later residual).
+template <int P>
+__device__ __forceinline__ void keep_raw(Ctx<P>& c, const float* v, float* dst) {
+#pragma unroll
+  for (int k = 0; k < kNormK; k++) {
+    int i = c.lane + 64 * k;
+    if (i < c.a.width) dst[i] = v[i];
   }
 }
 
@@ -220,17 +259,24 @@ __device__ __forceinline__ Own own_units(const Mv& m, int grid, int g) {
   return {first, end > first ? end - first : 0};
 }
 
+// Stage the inputs of phase p into LDS buffer `buf` (control wave). The OUT and DOWN
+// residuals read x as it was staged for this layer's QKV (xres[0]) and GATEUP (xres[1])
+// phases: a fused step keeps that raw copy in LDS from the earlier staging (`resident`);
+// a one-phase launch polls its own rows of it instead.
 template <int P, int A>
-__device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p, int buf) {
+__device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p, int buf, bool resident) {
   const StepArgs& a = c.a;
   float* xs = c.lds.xs[buf];
-  // What to poll: up to three whole vectors, an optional range of own rows, an optional norm.
+  // What to poll: up to three whole vectors and an optional range of own rows; then keep a
+  // raw copy and/or normalize.
   uint32_t vec[3];
   float* dst[3];
   int nvec = 0, n = a.width, n_p = a.width_p;
   unsigned ep = 0, ep_own = 0;
-  uint32_t norm_w = 0;
+  float* raw = nullptr;
+  float* own_dst = nullptr;
   bool norm = false;
+  float nw[kNormK];
   Own own{0, 0};
   if (p.kind == kAttn) {
     if constexpr (A == 1) return;
@@ -243,11 +289,12 @@ __device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p, int buf) {
     if (c.g != 0) return;
     ep = c.epoch(ph_index(kDown, a.layers - 1));
     vec[0] = a.t_x; dst[0] = xs; nvec = 1;
-    norm = true; norm_w = a.w_final_norm;
+    norm = true;
+    load_norm(c, a.w_final_norm, nw);
   } else {
     Mv m = matvec_of<P>(a, p);
     Own mine = own_units<P>(m, c.grid, c.g);
-    if (mine.count == 0) return;
+    if (mine.count == 0 && !resident) return;
     switch (p.kind) {
       case kInput: {
         __amdgpu_buffer_rsrc_t ir = make_rsrc(c.input, (uint32_t)a.features_p * 4u);
@@ -258,29 +305,42 @@ __device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p, int buf) {
       case kQkv:
         ep = c.epoch(ph_x_before(p.layer));
         vec[0] = a.t_x; dst[0] = xs; nvec = 1;
-        norm = true; norm_w = a.layer[p.layer].norm1;
+        norm = true;
+        load_norm(c, a.layer[p.layer].norm1, nw);
+        if (resident) raw = c.lds.xres[0];
         break;
       case kOut:
+        if (mine.count == 0) return;
         ep = c.epoch(ph_index(kAttn, p.layer));
         vec[0] = a.t_attn; dst[0] = xs; nvec = 1;
-        own = mine; ep_own = c.epoch(ph_x_before(p.layer));
+        if (!resident) {
+          own = mine; ep_own = c.epoch(ph_x_before(p.layer));
+          own_dst = c.lds.xres[0] + mine.first;
+        }
         break;
       case kGateUp:
         ep = c.epoch(ph_index(kOut, p.layer));
         vec[0] = a.t_x; dst[0] = xs; nvec = 1;
-        norm = true; norm_w = a.layer[p.layer].norm2;
+        norm = true;
+        load_norm(c, a.layer[p.layer].norm2, nw);
+        if (resident) raw = c.lds.xres[1];
         break;
       default:  // kDown
+        if (mine.count == 0) return;
         ep = c.epoch(ph_index(kGateUp, p.layer));
         vec[0] = a.t_act; dst[0] = xs; nvec = 1;
         n = a.ffn; n_p = a.ffn_p;
-        own = mine; ep_own = c.epoch(ph_index(kOut, p.layer));
+        if (!resident) {
+          own = mine; ep_own = c.epoch(ph_index(kOut, p.layer));
+          own_dst = c.lds.xres[1] + mine.first;
+        }
         break;
     }
   }
   for (int v = 0; v < nvec; v++) poll_vector(c, vec[v], n, n_p, ep, dst[v]);
-  if (own.count) poll_range(c, a.t_x, own.first, own.count, ep_own, c.lds.xres[buf]);
-  if (norm) norm_in_lds(c, xs, norm_w);
+  if (own.count) poll_range(c, a.t_x, own.first, own.count, ep_own, own_dst);
+  if (raw) keep_raw(c, xs, raw);
+  if (norm) norm_in_lds(c, xs, nw);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -363,9 +423,9 @@ __device__ __forceinline__ void prefetch(Ctx<P>& c, Phase p, uint4 (&ring)[kPF])
   }
 }
 
-// Epilogue of one unit (lane 0 only); s0/s1 are the row sums, xres the own rows of x.
+// Epilogue of one unit (lane 0 only); s0/s1 are the row sums, xres the x of the residual.
 template <int P>
-__device__ __forceinline__ void epilogue(Ctx<P>& c, Phase p, int unit, float s0, float s1, const float* xres, int first) {
+__device__ __forceinline__ void epilogue(Ctx<P>& c, Phase p, int unit, float s0, float s1, const float* xres) {
   const StepArgs& a = c.a;
   const unsigned ep = c.epoch(ph_index(p.kind, p.layer));
   switch (p.kind) {
@@ -394,7 +454,7 @@ __device__ __forceinline__ void epilogue(Ctx<P>& c, Phase p, int unit, float s0,
       break;
     }
     case kOut:
-      c.tstore(a.t_x + unit, ep, cast<P>(xres[unit - first] + cast<P>(s0)));
+      c.tstore(a.t_x + unit, ep, cast<P>(xres[unit] + cast<P>(s0)));
       break;
     case kGateUp: {
       float gv = cast<P>(s0), uv = cast<P>(s1);
@@ -402,7 +462,7 @@ __device__ __forceinline__ void epilogue(Ctx<P>& c, Phase p, int unit, float s0,
       break;
     }
     case kDown: {
-      float v = cast<P>(xres[unit - first] + cast<P>(s0));
+      float v = cast<P>(xres[unit] + cast<P>(s0));
       c.tstore(a.t_x + unit, ep, v);
       c.sstore(a.s_hidden + (uint32_t)p.layer * a.width + unit, v);
       break;
@@ -419,18 +479,22 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* 
   int unit;
   WaveWork w = work_of<P>(m, c.grid, c.g, c.wave - 1, unit);
   if (w.slabs == 0) return;
-  const int first = own_units<P>(m, c.grid, c.g).first;
   float (*sums)[2] = c.lds.sums[c.wave - 1];
   SlabCursor refill = cursor_at(w, kPF);
   int ru = 0, s = 0;  // row within the unit, slab within the row
   float acc0 = 0.f, acc1 = 0.f;
   const float* xs = xs_buf + c.lane * Traits<P>::kEpc;
+  if (c.wave == 1) stamp(c, p, 4);
   for (int base = 0; base < w.slabs; base += kPF) {
     int finished = 0;  // units completed in this pass of the ring
 #pragma unroll
     for (int j = 0; j < kPF; j++) {
       if (base + j < w.slabs) {
         float d = chunk_dot<P>(ring[j], xs + s * 64 * Traits<P>::kEpc);
+        if (j == 0 && base == 0 && c.a.stamps && c.wave == 1) {
+          asm volatile("" ::"v"(d));
+          stamp(c, p, 5);
+        }
         if (ru == 0) acc0 += d; else acc1 += d;
         if (base + j + kPF < w.slabs) {
           ring[j] = ld16(c.wr, refill.offset(c.lane));
@@ -455,9 +519,10 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* 
     }
     // Epilogues of the finished units, outside the unrolled loop (one copy of the code).
     if (c.lane == 0)
-      for (int k = 0; k < finished; k++) epilogue(c, p, unit + kStreamWaves * k, sums[k][0], sums[k][1], xres, first);
+      for (int k = 0; k < finished; k++) epilogue(c, p, unit + kStreamWaves * k, sums[k][0], sums[k][1], xres);
     unit += kStreamWaves * finished;
   }
+  if (c.wave == 1) stamp(c, p, 6);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -625,6 +690,7 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
         }
         __builtin_amdgcn_s_sleep(kPollSleep);
       }
+      if (c.wave == 1) stamp(c, p, 4);
 #pragma unroll
       for (int k = 0; k < E / 2; k++) {
         q[2 * k] = __builtin_bit_cast(float, pq[k].x);
@@ -686,7 +752,9 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
       c.sstore(pbase, mx);
       c.sstore(pbase + 1, total);
     }
+    if (c.wave == 1) stamp(c, p, 5);
     attn_publish_and_combine(c, w, p.layer, h, nactive, scale);
+    if (c.wave == 1) stamp(c, p, 6);
     __builtin_amdgcn_wave_barrier();
   }
 }
@@ -817,7 +885,7 @@ __device__ __forceinline__ void compute(Ctx<P>& c, Phase p, int buf, uint4 (&rin
     if constexpr (A == 1) compute_attn_regs(c, p, ring);
     else compute_attn_lds(c, p, ring);
   } else if (p.kind != kFinal) {
-    compute_matvec(c, p, c.lds.xs[buf], c.lds.xres[buf], ring);
+    compute_matvec(c, p, c.lds.xs[buf], c.lds.xres[p.kind == kDown ? 1 : 0], ring);
   }
 }
 
@@ -841,7 +909,7 @@ __global__ __launch_bounds__(kThreads) void phase_kernel(const StepArgs* __restr
   c.set_position(load_position(a));
   uint4 ring[kPF];
   for (int i = threadIdx.x; i < a.dim / 2; i += kThreads) c.lds.rope[i] = a.rope_freq[i];
-  if (c.wave == 0) stage_inputs<P, A>(c, p, 0);
+  if (c.wave == 0) stage_inputs<P, A>(c, p, 0, false);
   else prefetch(c, p, ring);
   lds_barrier();
   if (p.kind == kFinal) {
@@ -860,31 +928,41 @@ template <int P, int A>
 __device__ __forceinline__ void forward(Ctx<P>& c, uint4 (&ring)[kPF]) {
   const StepArgs& a = c.a;
   const int nph = ph_final(a) + 1;
-  const bool stamp = a.stamps && c.g == 0 && threadIdx.x == 0;
+  // Optional wall-clock stamps, per phase and workgroup: [start, stream wave 1 done, all
+  // stream waves done (staging starts), staging done]; the step end follows the last phase.
+  const bool stamp = a.stamps && threadIdx.x == 0;
+  unsigned long long* st = a.stamps + kStamps * c.g;
+  const int sst = kStamps * c.grid;
   if (threadIdx.x == 0) {
     c.lds.done[0] = 0;
     c.lds.done[1] = 0;
+    c.lds.staged = 0;
   }
   for (int i = threadIdx.x; i < a.dim / 2; i += kThreads) c.lds.rope[i] = a.rope_freq[i];
-  if (c.wave == 0) stage_inputs<P, A>(c, phase_of(a, 0), 0);
+  if (c.wave == 0) stage_inputs<P, A>(c, phase_of(a, 0), 0, true);
   else prefetch(c, phase_of(a, 0), ring);
-  // Optional stamps (workgroup 0): per phase [start, first stream wave done, staging
-  // started, staging done]; the end of the step follows the last phase.
-  const bool stamp_wave = a.stamps && c.g == 0 && c.lane == 0;
+  const bool stamp_wave = a.stamps && c.lane == 0;
   for (int ph = 0; ph < nph; ph++) {
     lds_barrier();
-    if (stamp) a.stamps[4 * ph] = wall_clock64();
+    if (stamp) put_stamp(st, sst * ph);
     Phase p = phase_of(a, ph);
     if (p.kind == kFinal) {
       if (c.g == 0 && c.wave == 0) compute_final(c, c.lds.xs[ph & 1]);
-      if (stamp) a.stamps[4 * nph] = wall_clock64();
+      if (stamp && c.g == 0) put_stamp(a.stamps, sst * nph);
       break;
     }
     if (c.wave != 0) {
       compute<P, A>(c, p, ph & 1, ring);
-      if (stamp_wave && c.wave == 1) a.stamps[4 * ph + 1] = wall_clock64();
-      prefetch(c, phase_of(a, ph + 1), ring);
+      if (stamp_wave && c.wave == 1) put_stamp(st, sst * ph + 1);
+      // Signal before issuing the next phase's prefetch: the issue itself can stall on a
+      // full memory pipeline, and the control wave can stage meanwhile.
       if (c.lane == 0) __hip_atomic_fetch_add(&c.lds.done[ph & 1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#if STAMD_ORDER == 3
+      while (__hip_atomic_load(&c.lds.staged, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)(ph + 1))
+        __builtin_amdgcn_s_sleep(1);
+#endif
+      prefetch(c, phase_of(a, ph + 1), ring);
+      if (stamp_wave && c.wave == 1) put_stamp(st, sst * ph + 7);
     } else {
       // Start polling for the next phase's inputs only once this workgroup's own part of
       // the current phase is done: the producers elsewhere finish at about the same time,
@@ -892,9 +970,13 @@ __device__ __forceinline__ void forward(Ctx<P>& c, uint4 (&ring)[kPF]) {
       while (__hip_atomic_load(&c.lds.done[ph & 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)kStreamWaves)
         __builtin_amdgcn_s_sleep(1);
       if (c.lane == 0) __hip_atomic_store(&c.lds.done[ph & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      if (stamp) a.stamps[4 * ph + 2] = wall_clock64();
-      stage_inputs<P, A>(c, phase_of(a, ph + 1), (ph + 1) & 1);
-      if (stamp) a.stamps[4 * ph + 3] = wall_clock64();
+      if (stamp) put_stamp(st, sst * ph + 2);
+      stage_inputs<P, A>(c, phase_of(a, ph + 1), (ph + 1) & 1, true);
+      if (stamp) put_stamp(st, sst * ph + 3);
+#if STAMD_ORDER == 3
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      if (c.lane == 0) __hip_atomic_store(&c.lds.staged, (unsigned)(ph + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#endif
     }
   }
 }

@@ -240,17 +240,21 @@ class Runtime:
         return float(mean.value), per
 
     def phase_times(self, event):
-        """One fused step with stamps (extension): (array [phases, 4] of microseconds since
-        the step started: phase start, first stream wave done, staging start, staging done;
+        """One fused step with stamps (extension): (array [phases, workgroups, 8] of
+        microseconds since workgroup 0 started the step: phase start, stream wave 1 done,
+        all stream waves done, staging done, three progress marks of stream wave 1, spare;
         step end)."""
         x = np.ascontiguousarray(event, dtype=np.float32)
-        n = 4 * (5 * self.config.layers + 2) + 1
-        out = np.empty(n, dtype=np.float64)
         count = ctypes.c_size_t(0)
-        _check(library().st_runtime_phase_times(self._handle(), _fptr(x),
-                                                out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), n,
-                                                ctypes.byref(count)))
-        return out[:-1].reshape(-1, 4), float(out[-1])
+        lib = library()
+        _check(lib.st_runtime_phase_times(self._handle(), _fptr(x), None, 0, ctypes.byref(count)))
+        n = count.value
+        out = np.empty(n, dtype=np.float64)
+        _check(lib.st_runtime_phase_times(self._handle(), _fptr(x),
+                                          out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), n,
+                                          ctypes.byref(count)))
+        phases = 5 * self.config.layers + 2
+        return out[:-1].reshape(phases, -1, 8), float(out[-1])
 
     def info(self) -> dict:
         return _json(library().st_runtime_info_json, self._handle())
