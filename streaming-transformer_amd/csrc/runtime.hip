@@ -205,7 +205,7 @@ class Runtime {
   hipStream_t stream_ = nullptr;
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;
-  DeviceBuffer weights_, keys_, values_, scratch_, tagged_, counters_, position_, epoch_, rope_, args_dev_;
+  DeviceBuffer weights_, keys_, values_, scratch_, tagged_, position_, epoch_, rope_, args_dev_;
   PinnedBuffer host_in_, host_out_;
   StepArgs args_{};
   const StepArgs* dargs_ = nullptr;
@@ -292,7 +292,6 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   a.s_input = take(a.features_p);
   a.s_hidden = take((size_t)c_.layers * c_.width);
   a.s_score = take(64);
-  a.s_partial = take((size_t)c_.heads * nch * (dim_ + 2));
   (void)vec;
   scratch_.alloc((size_t)off * 4);
   HIP_CHECK(hipMemset(scratch_.ptr, 0, (size_t)off * 4));
@@ -316,14 +315,14 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   a.t_attn = ttake(a.width_p);
   a.t_act = ttake(a.ffn_p);
   a.t_done = ttake(64);
+  a.t_po = ttake((size_t)c_.heads * nch * dim_);
+  a.t_pm = ttake((size_t)c_.heads * nch);
+  a.t_ps = ttake((size_t)c_.heads * nch);
   tagged_.alloc((size_t)toff * 8);
   HIP_CHECK(hipMemset(tagged_.ptr, 0, (size_t)toff * 8));
   a.tagged = reinterpret_cast<unsigned long long*>(tagged_.ptr);
   a.tagged_bytes = toff * 8;
 
-  counters_.alloc((size_t)c_.heads * 32 * 4);
-  HIP_CHECK(hipMemset(counters_.ptr, 0, counters_.bytes));
-  a.head_count = reinterpret_cast<unsigned*>(counters_.ptr);
   position_.alloc(8);
   HIP_CHECK(hipMemset(position_.ptr, 0, 8));
   a.position = reinterpret_cast<unsigned long long*>(position_.ptr);
@@ -488,8 +487,11 @@ void Runtime::build_weights(const st_tensor* tensors, size_t count) {
 template <int P, int A>
 void Runtime::launch_phases_t() {
   const int nph = 5 * c_.layers + 2;
+  // Attention chunks of one head are combined by polling partials written in the same
+  // launch, so every workgroup of a launch must be resident at once.
+  const int resident = std::min(grid_, legal_blocks_);
   for (int ph = 0; ph < nph; ph++) {
-    int grid = ph == nph - 1 ? 1 : grid_;
+    int grid = ph == nph - 1 ? 1 : resident;
     hipLaunchKernelGGL((phase_kernel<P, A>), dim3(grid), dim3(kThreads), 0, stream_, dargs_, ph);
   }
   HIP_CHECK(hipGetLastError());

@@ -74,13 +74,13 @@ struct StepArgs {
   uint32_t cache_bytes;            // bytes of one of keys/values
   float* scratch;                  // fp32 scratch arena (agent-coherent access)
   uint32_t scratch_bytes;
-  // scratch offsets (floats): host-staged input, hidden state, score, attention partials
-  uint32_t s_input, s_hidden, s_score, s_partial;
+  // scratch offsets (floats): host-staged input, hidden state, score
+  uint32_t s_input, s_hidden, s_score;
   // tagged vectors (8-byte elements: epoch << 32 | float bits)
   unsigned long long* tagged;
   uint32_t tagged_bytes;
   uint32_t t_x, t_q, t_k, t_v, t_attn, t_act, t_done;  // element offsets
-  unsigned* head_count;            // [H] * 32 words apart (wrapping chunk counters)
+  uint32_t t_po, t_pm, t_ps;       // attention partials per item: o [items][dh], max, exp sum
   unsigned long long* position;
   unsigned* epoch;                 // epoch of phase 0 of the next step
   unsigned* error;                 // sticky error bits

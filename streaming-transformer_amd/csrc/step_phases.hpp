@@ -18,22 +18,17 @@
 
 #include "step_device.hpp"
 
-#ifndef STAMD_ORDER
-#define STAMD_ORDER 1
-#endif
-
 namespace stamd {
 
 struct LdsAll {
   float xs[2][kXs];                      // phase input vector, double buffered by phase parity
   float xres[2][kMaxDim];                // x before this layer (OUT residual) and after OUT (DOWN residual)
   float qkv[3 * kMaxDim];                // attention LDS path: q, k, v of the step
-  float stage[kStreamWaves][kAttnLds];   // attention LDS path: per-wave K/V staging; combine scale
+  float stage[kStreamWaves][kAttnLds];   // attention LDS path: per-wave K/V staging
   float probs[kStreamWaves][64];
   float sums[kStreamWaves][kPF][2];      // row sums of units finished in the current ring pass
   float rope[kMaxDim / 2];               // RoPE inverse frequencies
   unsigned done[2];                      // stream waves finished with the phase of this parity
-  unsigned staged;                       // phases whose successor's inputs are staged
 };
 
 template <int P>
@@ -71,17 +66,33 @@ struct Ctx {
     v2i w = {__builtin_bit_cast(int, v), (int)ep};
     __builtin_amdgcn_raw_buffer_store_b64(w, tr, (int)(index * 8u), 0, kSc1);
   }
+  __device__ __forceinline__ uint2 tload(uint32_t index) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(tr, (int)(index * 8u), 0, kSc1));
+  }
   __device__ __forceinline__ void timeout() {
     if (lane == 0) __hip_atomic_fetch_or(a.error, kErrPollTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     dead = true;
   }
+  // True once a poll started at `start` has run past the spin limit (and records it).
+  __device__ __forceinline__ bool expired(unsigned long long start) {
+    if (wall_clock64() - start > a.spin_limit) {
+      timeout();
+      return true;
+    }
+    return false;
+  }
 };
 
+// Position and epoch are read by every lane; readfirstlane tells the compiler they are
+// wave-uniform, so everything derived from them (attention geometry, offsets) stays in
+// scalar registers.
 __device__ __forceinline__ unsigned long long load_position(const StepArgs& a) {
-  return __hip_atomic_load(a.position, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  unsigned long long v = __hip_atomic_load(a.position, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v), hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+  return ((unsigned long long)hi << 32) | lo;
 }
 __device__ __forceinline__ unsigned load_epoch(const StepArgs& a) {
-  return __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __builtin_amdgcn_readfirstlane(__hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
 // Phase indices within a step.
@@ -528,79 +539,121 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* 
 // ---------------------------------------------------------------------------------------------
 // stream waves: attention (src/cuda/Primitives.cuh:167-219, src/cpu/Cpu.cpp:97-109)
 
-// Count one chunk partial of head h (after this wave's partial stores are complete); the
-// last chunk of the head to arrive combines all partials in chunk order,
-//   attn = sum_c o_c exp(m_c - M) / sum_c s_c exp(m_c - M),
-// and publishes attn_h. The wrapping increment leaves the counter at 0 for the next use.
+// Publish the (max logit, exp sum) of item `it` as tagged elements t_pm / t_ps[it]; the
+// item's o[dim] goes to t_po[it * dim ..].
 template <int P>
-__device__ __forceinline__ void attn_publish_and_combine(Ctx<P>& c, const AttnWork& w, int layer, int h, int nactive,
-                                                         float* scale) {
+__device__ __forceinline__ void publish_stats(Ctx<P>& c, unsigned ep, int it, float m, float s) {
+  if (c.lane == 0) {
+    c.tstore(c.a.t_pm + (uint32_t)it, ep, m);
+    c.tstore(c.a.t_ps + (uint32_t)it, ep, s);
+  }
+}
+
+__device__ __forceinline__ float lane_value(float v, int k) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), k));
+}
+
+// Combine the chunk partials of head h (done by the wave that computed chunk 0, after all
+// of its own items, so no wave waits on work queued behind its own wait), in chunk order:
+//   attn = sum_c o_c exp(m_c - M) / sum_c s_c exp(m_c - M),  M = max_c m_c,
+// then publish attn_h. Polls the tagged partials.
+template <int P>
+__device__ __forceinline__ void combine_head(Ctx<P>& c, int layer, int h, int nch, int nactive) {
   const StepArgs& a = c.a;
   const int dim = a.dim;
-  __builtin_amdgcn_s_waitcnt(0);
-  unsigned old = 0;
-  if (c.lane == 0)
-    old = __builtin_amdgcn_atomic_inc32(a.head_count + h * 32, (unsigned)(nactive - 1), __ATOMIC_RELAXED, "agent");
-  old = __shfl(old, 0);
-  if ((int)old != nactive - 1) return;
   const unsigned ep = c.epoch(ph_index(kAttn, layer));
-  const uint32_t hb = a.s_partial + (uint32_t)(h * w.nch) * (uint32_t)(dim + 2);
-  const uint32_t pstride = (uint32_t)(dim + 2);
-  float big = -INFINITY, denom = 0.f;
-  if (nactive <= 32 && dim <= 64) {
-    // one round of loads: (m_c, s_c) per lane, o_c[lane] for every chunk
-    int cl = c.lane < nactive ? c.lane : nactive - 1;
-    float mc = c.sload(hb + (uint32_t)cl * pstride);
-    float sc = c.sload(hb + (uint32_t)cl * pstride + 1u);
-    int il = c.lane < dim ? c.lane : dim - 1;
-    float part[32];
-#pragma unroll
-    for (int k = 0; k < 32; k++) {
-      int cc = k < nactive ? k : nactive - 1;
-      part[k] = c.sload(hb + (uint32_t)cc * pstride + 2u + (uint32_t)il);
+  const uint32_t item0 = (uint32_t)(h * nch);
+  if (nactive <= 64 && dim <= 64) {
+    // Lane c polls (m_c, s_c); then lane i reads o_c[i] of the chunks in groups of 8.
+    const int cl = c.lane < nactive ? c.lane : nactive - 1;
+    const int il = c.lane < dim ? c.lane : dim - 1;
+    uint2 pm, ps;
+    unsigned long long start = wall_clock64();
+    while (true) {
+      pm = c.tload(a.t_pm + item0 + (uint32_t)cl);
+      ps = c.tload(a.t_ps + item0 + (uint32_t)cl);
+      if (__all(pm.y == ep && ps.y == ep) || c.dead || c.expired(start)) break;
+      __builtin_amdgcn_s_sleep(kPollSleep);
     }
-    big = wave_max(c.lane < nactive ? mc : -INFINITY);
-    float e = c.lane < nactive ? expf(mc - big) : 0.f;
-    denom = wave_sum(sc * e);
-    scale[c.lane] = e;
-    __builtin_amdgcn_wave_barrier();
+    const float mc = __builtin_bit_cast(float, pm.x), sc = __builtin_bit_cast(float, ps.x);
+    const float big = wave_max(c.lane < nactive ? mc : -INFINITY);
+    const float e = c.lane < nactive ? expf(mc - big) : 0.f;
+    const float denom = wave_sum(sc * e);
     float o = 0.f;
+    for (int k0 = 0; k0 < nactive; k0 += 8) {
+      uint2 po[8];
+      start = wall_clock64();
+      while (true) {
+        bool ok = true;
 #pragma unroll
-    for (int k = 0; k < 32; k++)
-      if (k < nactive) o += part[k] * scale[k];
-    if (c.lane < dim) c.tstore(a.t_attn + h * dim + c.lane, ep, cast<P>(o / denom));
-  } else {
-    for (int c0 = 0; c0 < nactive; c0 += 64) {
-      int cc = c0 + c.lane;
-      float mc = cc < nactive ? c.sload(hb + (uint32_t)cc * pstride) : -INFINITY;
-      big = fmaxf(big, mc);
-      if (cc < nactive) scale[cc] = mc;
-    }
-    big = wave_max(big);
-    for (int c0 = 0; c0 < nactive; c0 += 64) {
-      int cc = c0 + c.lane;
-      float sc = cc < nactive ? c.sload(hb + (uint32_t)cc * pstride + 1u) : 0.f;
-      float e = cc < nactive ? expf(scale[cc] - big) : 0.f;
-      if (cc < nactive) scale[cc] = e;
-      denom += sc * e;
-    }
-    denom = wave_sum(denom);
-    __builtin_amdgcn_wave_barrier();
-    for (int i = c.lane; i < dim; i += 64) {
-      float o = 0.f;
-      for (int c0 = 0; c0 < nactive; c0 += 16) {
-        float part[16];
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-          int cc = c0 + k < nactive ? c0 + k : nactive - 1;
-          part[k] = c.sload(hb + (uint32_t)cc * pstride + 2u + (uint32_t)i);
+        for (int k = 0; k < 8; k++) {
+          int cc = k0 + k < nactive ? k0 + k : nactive - 1;
+          po[k] = c.tload(a.t_po + (item0 + (uint32_t)cc) * (uint32_t)dim + (uint32_t)il);
         }
 #pragma unroll
-        for (int k = 0; k < 16; k++)
-          if (c0 + k < nactive) o += part[k] * scale[c0 + k];
+        for (int k = 0; k < 8; k++) ok = ok && po[k].y == ep;
+        if (__all(ok) || c.dead || c.expired(start)) break;
+        __builtin_amdgcn_s_sleep(kPollSleep);
       }
-      c.tstore(a.t_attn + h * dim + i, ep, cast<P>(o / denom));
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        if (k0 + k < nactive) o += __builtin_bit_cast(float, po[k].x) * lane_value(e, k0 + k);
     }
+    if (c.lane < dim) c.tstore(a.t_attn + h * dim + c.lane, ep, cast<P>(o / denom));
+    return;
+  }
+  // General sizes: wait for every chunk's statistics, then maxima, denominators and outputs
+  // in chunk order.
+  for (int c0 = 0; c0 < nactive; c0 += 64) {
+    const int cc = c0 + c.lane < nactive ? c0 + c.lane : nactive - 1;
+    unsigned long long start = wall_clock64();
+    while (true) {
+      uint2 vm = c.tload(a.t_pm + item0 + (uint32_t)cc);
+      uint2 vs = c.tload(a.t_ps + item0 + (uint32_t)cc);
+      if (__all(vm.y == ep && vs.y == ep) || c.dead || c.expired(start)) break;
+      __builtin_amdgcn_s_sleep(kPollSleep);
+    }
+  }
+  float big = -INFINITY;
+  for (int c0 = 0; c0 < nactive; c0 += 64) {
+    int cc = c0 + c.lane;
+    if (cc < nactive) big = fmaxf(big, __builtin_bit_cast(float, c.tload(a.t_pm + item0 + (uint32_t)cc).x));
+  }
+  big = wave_max(big);
+  float denom = 0.f;
+  for (int c0 = 0; c0 < nactive; c0 += 64) {
+    int cc = c0 + c.lane;
+    if (cc < nactive) {
+      float mc = __builtin_bit_cast(float, c.tload(a.t_pm + item0 + (uint32_t)cc).x);
+      float sc = __builtin_bit_cast(float, c.tload(a.t_ps + item0 + (uint32_t)cc).x);
+      denom += sc * expf(mc - big);
+    }
+  }
+  denom = wave_sum(denom);
+  for (int i = c.lane; i < dim; i += 64) {
+    float o = 0.f;
+    for (int cc = 0; cc < nactive; cc++) {
+      unsigned long long start = wall_clock64();
+      uint2 vo;
+      while (true) {
+        vo = c.tload(a.t_po + (item0 + (uint32_t)cc) * (uint32_t)dim + (uint32_t)i);
+        if (vo.y == ep || c.dead || c.expired(start)) break;
+        __builtin_amdgcn_s_sleep(kPollSleep);
+      }
+      float mc = __builtin_bit_cast(float, c.tload(a.t_pm + item0 + (uint32_t)cc).x);
+      o += __builtin_bit_cast(float, vo.x) * expf(mc - big);
+    }
+    c.tstore(a.t_attn + h * dim + i, ep, cast<P>(o / denom));
+  }
+}
+
+// Combines owed by this wave: the heads whose chunk 0 it computed in this phase.
+template <int P>
+__device__ __forceinline__ void combine_owned(Ctx<P>& c, Phase p, const AttnWork& w, int nactive) {
+  for (int m = 0; m < w.items; m++) {
+    int it = w.wid + w.nw * m;
+    int h = it / w.nch, ch = it - h * w.nch;
+    if (ch == 0) combine_head(c, p.layer, h, w.nch, nactive);
   }
 }
 
@@ -655,7 +708,6 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
   const int nactive = (c.valid + chunk - 1) / chunk;
   const float div = sqrtf((float)dim);
   const unsigned ep_qkv = c.epoch(ph_index(kQkv, p.layer));
-  float* scale = c.lds.stage[c.wave - 1];
   for (int m = 0; m < w.items; m++) {
     int it = w.wid + w.nw * m;
     int h = it / w.nch, ch = it - h * w.nch;
@@ -743,20 +795,17 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
 #pragma unroll
     for (int e = 0; e < E; e++)
       for (int o = 32; o >= group; o >>= 1) out[e] += __shfl_xor(out[e], o);
-    uint32_t pbase = a.s_partial + ((uint32_t)(h * w.nch + ch)) * (uint32_t)(dim + 2);
+    const unsigned ep = c.epoch(ph_index(kAttn, p.layer));
     if (c.lane < group) {
+      const uint32_t ob = (uint32_t)it * (uint32_t)dim + (uint32_t)col0;
 #pragma unroll
-      for (int e = 0; e < E; e++) c.sstore(pbase + 2 + col0 + e, out[e]);
+      for (int e = 0; e < E; e++) c.tstore(a.t_po + ob + (uint32_t)e, ep, out[e]);
     }
-    if (c.lane == 0) {
-      c.sstore(pbase, mx);
-      c.sstore(pbase + 1, total);
-    }
+    publish_stats(c, ep, it, mx, total);
     if (c.wave == 1) stamp(c, p, 5);
-    attn_publish_and_combine(c, w, p.layer, h, nactive, scale);
-    if (c.wave == 1) stamp(c, p, 6);
-    __builtin_amdgcn_wave_barrier();
   }
+  combine_owned(c, p, w, nactive);
+  if (c.wave == 1) stamp(c, p, 6);
 }
 
 // Write a prefetched K or V block (register ring half) into this wave's LDS stage as
@@ -841,19 +890,16 @@ __device__ __forceinline__ void compute_attn_lds(Ctx<P>& c, Phase p, uint4 (&rin
     if (cur >= 0 && cur < chunk)
       for (int i = c.lane; i < dim; i += 64) stage[cur * stride + i] = v_cur[h * dim + i];
     __builtin_amdgcn_wave_barrier();
-    uint32_t pbase = a.s_partial + ((uint32_t)(h * w.nch + ch)) * (uint32_t)(dim + 2);
+    const unsigned ep = c.epoch(ph_index(kAttn, p.layer));
     for (int i = c.lane; i < dim; i += 64) {
       float o = 0.f;
       for (int j = 0; j < rows; j++) o += probs[j] * stage[j * stride + i];
-      c.sstore(pbase + 2 + i, o);
+      c.tstore(a.t_po + (uint32_t)it * (uint32_t)dim + (uint32_t)i, ep, o);
     }
-    if (c.lane == 0) {
-      c.sstore(pbase, mx);
-      c.sstore(pbase + 1, total);
-    }
-    attn_publish_and_combine(c, w, p.layer, h, nactive, stage);
+    publish_stats(c, ep, it, mx, total);
     __builtin_amdgcn_wave_barrier();
   }
+  combine_owned(c, p, w, nactive);
 }
 
 // Final phase (workgroup 0, control wave): score = W_score . norm(x), not cast; position++.
@@ -923,62 +969,73 @@ __global__ __launch_bounds__(kThreads) void phase_kernel(const StepArgs* __restr
   if (c.wave != 0) compute<P, A>(c, p, 0, ring);
 }
 
-// One forward over the device-held state with the context's position and epoch base.
+// Control wave of one forward: stage each phase's inputs once this workgroup's stream
+// waves are done with the previous phase. One barrier per phase, matching stream_loop.
 template <int P, int A>
-__device__ __forceinline__ void forward(Ctx<P>& c, uint4 (&ring)[kPF]) {
+__device__ __forceinline__ void control_loop(Ctx<P>& c, int nph) {
   const StepArgs& a = c.a;
-  const int nph = ph_final(a) + 1;
-  // Optional wall-clock stamps, per phase and workgroup: [start, stream wave 1 done, all
-  // stream waves done (staging starts), staging done]; the step end follows the last phase.
-  const bool stamp = a.stamps && threadIdx.x == 0;
+  // Optional wall-clock stamps (slots as in stamp()); the step end follows the last phase.
+  const bool stamps = a.stamps && threadIdx.x == 0;
   unsigned long long* st = a.stamps + kStamps * c.g;
   const int sst = kStamps * c.grid;
+  stage_inputs<P, A>(c, phase_of(a, 0), 0, true);
+  for (int ph = 0; ph < nph; ph++) {
+    lds_barrier();
+    if (stamps) put_stamp(st, sst * ph);
+    Phase p = phase_of(a, ph);
+    if (p.kind == kFinal) {
+      if (c.g == 0) compute_final(c, c.lds.xs[ph & 1]);
+      if (stamps && c.g == 0) put_stamp(a.stamps, sst * nph);
+      break;
+    }
+    // Start polling for the next phase's inputs only once this workgroup's own part of
+    // the current phase is done: the producers elsewhere finish at about the same time,
+    // and polling earlier would only add memory traffic.
+    while (__hip_atomic_load(&c.lds.done[ph & 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)kStreamWaves)
+      __builtin_amdgcn_s_sleep(1);
+    if (c.lane == 0) __hip_atomic_store(&c.lds.done[ph & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (stamps) put_stamp(st, sst * ph + 2);
+    stage_inputs<P, A>(c, phase_of(a, ph + 1), (ph + 1) & 1, true);
+    if (stamps) put_stamp(st, sst * ph + 3);
+  }
+}
+
+// Stream wave of one forward: compute each phase from the register ring, then prefetch
+// the next phase's first slabs while the control wave stages its inputs.
+template <int P, int A>
+__device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
+  const StepArgs& a = c.a;
+  const bool stamps = a.stamps && c.wave == 1 && c.lane == 0;
+  unsigned long long* st = a.stamps + kStamps * c.g;
+  const int sst = kStamps * c.grid;
+  uint4 ring[kPF];
+  prefetch(c, phase_of(a, 0), ring);
+  for (int ph = 0; ph < nph; ph++) {
+    lds_barrier();
+    Phase p = phase_of(a, ph);
+    if (p.kind == kFinal) break;
+    compute<P, A>(c, p, ph & 1, ring);
+    if (stamps) put_stamp(st, sst * ph + 1);
+    // Signal before issuing the next phase's prefetch: the issue itself can stall on a
+    // full memory pipeline, and the control wave can stage meanwhile.
+    if (c.lane == 0) __hip_atomic_fetch_add(&c.lds.done[ph & 1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    prefetch(c, phase_of(a, ph + 1), ring);
+    if (stamps) put_stamp(st, sst * ph + 7);
+  }
+}
+
+// One forward over the device-held state with the context's position and epoch base.
+template <int P, int A>
+__device__ __forceinline__ void forward(Ctx<P>& c) {
+  const StepArgs& a = c.a;
+  const int nph = ph_final(a) + 1;
   if (threadIdx.x == 0) {
     c.lds.done[0] = 0;
     c.lds.done[1] = 0;
-    c.lds.staged = 0;
   }
   for (int i = threadIdx.x; i < a.dim / 2; i += kThreads) c.lds.rope[i] = a.rope_freq[i];
-  if (c.wave == 0) stage_inputs<P, A>(c, phase_of(a, 0), 0, true);
-  else prefetch(c, phase_of(a, 0), ring);
-  const bool stamp_wave = a.stamps && c.lane == 0;
-  for (int ph = 0; ph < nph; ph++) {
-    lds_barrier();
-    if (stamp) put_stamp(st, sst * ph);
-    Phase p = phase_of(a, ph);
-    if (p.kind == kFinal) {
-      if (c.g == 0 && c.wave == 0) compute_final(c, c.lds.xs[ph & 1]);
-      if (stamp && c.g == 0) put_stamp(a.stamps, sst * nph);
-      break;
-    }
-    if (c.wave != 0) {
-      compute<P, A>(c, p, ph & 1, ring);
-      if (stamp_wave && c.wave == 1) put_stamp(st, sst * ph + 1);
-      // Signal before issuing the next phase's prefetch: the issue itself can stall on a
-      // full memory pipeline, and the control wave can stage meanwhile.
-      if (c.lane == 0) __hip_atomic_fetch_add(&c.lds.done[ph & 1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-#if STAMD_ORDER == 3
-      while (__hip_atomic_load(&c.lds.staged, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)(ph + 1))
-        __builtin_amdgcn_s_sleep(1);
-#endif
-      prefetch(c, phase_of(a, ph + 1), ring);
-      if (stamp_wave && c.wave == 1) put_stamp(st, sst * ph + 7);
-    } else {
-      // Start polling for the next phase's inputs only once this workgroup's own part of
-      // the current phase is done: the producers elsewhere finish at about the same time,
-      // and polling earlier would only add memory traffic.
-      while (__hip_atomic_load(&c.lds.done[ph & 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)kStreamWaves)
-        __builtin_amdgcn_s_sleep(1);
-      if (c.lane == 0) __hip_atomic_store(&c.lds.done[ph & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      if (stamp) put_stamp(st, sst * ph + 2);
-      stage_inputs<P, A>(c, phase_of(a, ph + 1), (ph + 1) & 1, true);
-      if (stamp) put_stamp(st, sst * ph + 3);
-#if STAMD_ORDER == 3
-      __builtin_amdgcn_s_waitcnt(0xc07f);
-      if (c.lane == 0) __hip_atomic_store(&c.lds.staged, (unsigned)(ph + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-#endif
-    }
-  }
+  if (c.wave == 0) control_loop<P, A>(c, nph);
+  else stream_loop<P, A>(c, nph);
 }
 
 // One step per launch (fused backend). `event` overrides the INPUT source when not null.
@@ -990,8 +1047,7 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(const StepArgs* __restr
   if (event) c.input = event;
   c.base = load_epoch(a);
   c.set_position(load_position(a));
-  uint4 ring[kPF];
-  forward<P, A>(c, ring);
+  forward<P, A>(c);
   if (blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_store(a.epoch, c.base + (unsigned)ph_final(a) + 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1009,7 +1065,6 @@ __global__ __launch_bounds__(kThreads) void trace_kernel(const StepArgs* __restr
   const unsigned base0 = load_epoch(a);
   const unsigned long long t0 = load_position(a);
   const unsigned per_step = (unsigned)ph_final(a) + 2u;  // phases + the step-done word
-  uint4 ring[kPF];
   for (int e = 0; e < count; e++) {
     if (blockIdx.x == 0 && threadIdx.x == 0) stamps[e] = wall_clock64();
     c.base = base0 + (unsigned)e * per_step;
@@ -1019,7 +1074,7 @@ __global__ __launch_bounds__(kThreads) void trace_kernel(const StepArgs* __restr
       float done[2];
       poll_pieces<P, 1>(c, a.t_done, 1, 0, 1, c.base - 1u, done);
     }
-    forward<P, A>(c, ring);
+    forward<P, A>(c);
     if (c.g == 0 && threadIdx.x == 0) c.tstore(a.t_done, c.base + per_step - 1u, 0.f);
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
@@ -1028,8 +1083,8 @@ __global__ __launch_bounds__(kThreads) void trace_kernel(const StepArgs* __restr
   }
 }
 
-// Zero K/V, hidden state, attention counters and the position (src/cuda/Primitives.cuh:280-292).
-// Tagged vectors keep their tags: epochs only grow.
+// Zero K/V, hidden state and the position (src/cuda/Primitives.cuh:280-292). Tagged vectors
+// keep their tags: epochs only grow.
 __global__ void reset_kernel(const StepArgs* __restrict__ ap) {
   const StepArgs& a = *ap;
   size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1041,7 +1096,6 @@ __global__ void reset_kernel(const StepArgs* __restrict__ ap) {
     v[i] = 0;
   }
   for (size_t i = tid; i < (size_t)a.layers * a.width; i += stride) a.scratch[a.s_hidden + i] = 0.f;
-  for (size_t i = tid; i < (size_t)a.heads * 32; i += stride) a.head_count[i] = 0;
   if (tid == 0) *a.position = 0;
 }
 

@@ -76,11 +76,16 @@ SHAPES = {
     # reference fixture shapes with head dim 32 (configs/main.json, configs/large.json)
     'ref-main': ModelConfig(2, 128, 4, 256, 256, 32),
     'ref-large': ModelConfig(4, 256, 8, 512, 512, 32),
+    # head dim 48 (not a power of two): attention reads K/V rows in place from the FIFO
+    'dh48': ModelConfig(2, 96, 2, 192, 40, 96),
+    # 48 active chunks per head at full window: the general partial-combine path
+    'long-window': ModelConfig(1, 128, 2, 256, 1536, 128),
 }
 
 
 @pytest.mark.parametrize('name,steps,reset_at', [('small', 160, 137), ('main', 40, None), ('large', 12, None),
-                                                 ('ref-main', 300, 261), ('ref-large', 64, None)])
+                                                 ('ref-main', 300, 261), ('ref-large', 64, None),
+                                                 ('dh48', 100, 57), ('long-window', 1540, None)])
 def test_fused_matches_oracle_at_shape(name, steps, reset_at):
     c = SHAPES[name]
     w = synthetic_checkpoint(c, seed=1)
@@ -100,7 +105,7 @@ def test_fused_matches_oracle_at_shape(name, steps, reset_at):
             assert numerical.fp32_strict_failures(a, o, **STRICT) == 0, float(np.abs(a - o).max())
 
 
-@pytest.mark.parametrize('name,steps', [('small', 150), ('main', 140), ('ref-main', 64)])
+@pytest.mark.parametrize('name,steps', [('small', 150), ('main', 140), ('ref-main', 64), ('dh48', 50)])
 def test_backends_are_bit_identical(name, steps):
     c = SHAPES[name]
     w = synthetic_checkpoint(c, seed=2)
