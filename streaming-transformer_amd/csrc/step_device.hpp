@@ -33,7 +33,12 @@ namespace stamd {
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kStreamWaves = kWaves - 1;
-constexpr int kPF = 16;            // register ring depth (slabs) per stream wave
+#ifndef STAMD_PF
+#define STAMD_PF 16
+#endif
+constexpr int kPF = STAMD_PF;      // register ring depth (slabs) per stream wave
+constexpr int kKB = 8;             // ring slabs per attention K (or V) block
+static_assert(2 * kKB <= kPF, "an attention item's K and V blocks fit in the ring");
 constexpr int kStamps = 8;         // wall-clock stamps per phase and workgroup (profiling only)
 constexpr int kMaxGrid = 1024;     // largest grid accepted
 constexpr int kMaxLayers = 16;

@@ -414,7 +414,7 @@ template <int P>
 __device__ __forceinline__ void load_block(Ctx<P>& c, __amdgpu_buffer_rsrc_t r, int layer, int h, int ch, int kchunks,
                                            uint4* part) {
 #pragma unroll
-  for (int j = 0; j < kPF / 2; j++) part[j] = ld16(r, attn_chunk_offset<P>(c.a, layer, h, ch, c.lane + 64 * j, kchunks));
+  for (int j = 0; j < kKB; j++) part[j] = ld16(r, attn_chunk_offset<P>(c.a, layer, h, ch, c.lane + 64 * j, kchunks));
 }
 
 template <int P>
@@ -425,7 +425,7 @@ __device__ __forceinline__ void prefetch(Ctx<P>& c, Phase p, uint4 (&ring)[kPF])
     if (w.items == 0) return;
     int h = w.wid / w.nch, ch = w.wid - h * w.nch;
     load_block<P>(c, c.kr, p.layer, h, ch, w.kchunks, ring);
-    load_block<P>(c, c.vr, p.layer, h, ch, w.kchunks, ring + kPF / 2);
+    load_block<P>(c, c.vr, p.layer, h, ch, w.kchunks, ring + kKB);
   } else if (p.kind != kFinal) {
     Mv m = matvec_of<P>(c.a, p);
     int unit0;
@@ -714,7 +714,7 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
     if (ch >= nactive) continue;
     if (m > 0) {
       load_block<P>(c, c.kr, p.layer, h, ch, w.kchunks, ring);
-      load_block<P>(c, c.vr, p.layer, h, ch, w.kchunks, ring + kPF / 2);
+      load_block<P>(c, c.vr, p.layer, h, ch, w.kchunks, ring + kKB);
     }
     // q, k, v of this lane's columns of head h (E each), polled from the tagged vectors.
     float q[E], kc[E], vc[E];
@@ -759,10 +759,10 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
 #pragma unroll
       for (int e = 0; e < E; e++) ring_write(c, p.layer, h, col0 + e, kc[e], vc[e]);
     }
-    float logit[kPF / 2];
+    float logit[kKB];
     float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kPF / 2; j++) {
+    for (int j = 0; j < kKB; j++) {
       int row = row_lane + j * rows_per_load;
       bool live = j < loads && (c.lane + 64 * j) < w.kchunks && row < chunk && row0 + row < c.valid;
       bool cur = row0 + row == c.slot;
@@ -781,13 +781,13 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
 #pragma unroll
     for (int e = 0; e < E; e++) out[e] = 0.f;
 #pragma unroll
-    for (int j = 0; j < kPF / 2; j++) {
+    for (int j = 0; j < kKB; j++) {
       float pr = logit[j] == -INFINITY ? 0.f : expf(logit[j] - mx);
       psum += pr;
       int row = row_lane + j * rows_per_load;
       bool cur = row0 + row == c.slot;
       float v[E];
-      kv_decode<P>(ring[kPF / 2 + j], v);
+      kv_decode<P>(ring[kKB + j], v);
 #pragma unroll
       for (int e = 0; e < E; e++) out[e] += pr * (cur ? vc[e] : v[e]);
     }
@@ -819,7 +819,7 @@ __device__ __forceinline__ void block_to_lds(Ctx<P>& c, const uint4* part, int k
   int row = (c.lane * kPer) / dim;
   int col = c.lane * kPer - row * dim;
 #pragma unroll
-  for (int j = 0; j < kPF / 2; j++) {
+  for (int j = 0; j < kKB; j++) {
     if (c.lane + 64 * j < kchunks) {
       float v[kPer];
       kv_decode<P>(part[j], v);
@@ -862,7 +862,7 @@ __device__ __forceinline__ void compute_attn_lds(Ctx<P>& c, Phase p, uint4 (&rin
     if (ch >= nactive) continue;
     if (m > 0) {
       load_block<P>(c, c.kr, p.layer, h, ch, w.kchunks, ring);
-      load_block<P>(c, c.vr, p.layer, h, ch, w.kchunks, ring + kPF / 2);
+      load_block<P>(c, c.vr, p.layer, h, ch, w.kchunks, ring + kKB);
     }
     int row0 = ch * chunk;
     int rows = c.valid - row0 < chunk ? c.valid - row0 : chunk;  // valid slots are [0, valid)
@@ -886,7 +886,7 @@ __device__ __forceinline__ void compute_attn_lds(Ctx<P>& c, Phase p, uint4 (&rin
     float total = wave_sum(pr);
     probs[c.lane] = pr;
     __builtin_amdgcn_wave_barrier();
-    block_to_lds<P>(c, ring + kPF / 2, w.kchunks, stage);
+    block_to_lds<P>(c, ring + kKB, w.kchunks, stage);
     if (cur >= 0 && cur < chunk)
       for (int i = c.lane; i < dim; i += 64) stage[cur * stride + i] = v_cur[h * dim + i];
     __builtin_amdgcn_wave_barrier();
