@@ -111,6 +111,34 @@ struct PinnedBuffer {
   }
 };
 
+// Coherent pinned host memory mapped into the device's address space (the persistent
+// backend's mailbox and event buffer).
+struct MappedBuffer {
+  void* ptr = nullptr;
+  void* dev = nullptr;
+  void alloc(size_t n) {
+    HIP_CHECK(hipHostMalloc(&ptr, std::max<size_t>(n, 64), hipHostMallocMapped | hipHostMallocCoherent));
+    std::memset(ptr, 0, std::max<size_t>(n, 64));
+    HIP_CHECK(hipHostGetDevicePointer(&dev, ptr, 0));
+  }
+  ~MappedBuffer() {
+    if (ptr) (void)hipHostFree(ptr);
+  }
+};
+
+// Host/device mailbox of the persistent backend (src/cuda/Primitives.cuh:16-23): request,
+// completion and exited words on separate 64-byte lines; only naturally aligned 64-bit
+// loads and stores cross the host/device boundary, no read-modify-write.
+struct alignas(64) Mailbox {
+  alignas(64) unsigned long long request;
+  alignas(64) unsigned long long completion;
+  alignas(64) unsigned long long exited;
+  alignas(64) int32_t command;
+  float score;
+  unsigned long long checksum;
+  uint32_t error;
+};
+
 static void validate_config(const st_config& c) {
   if (c.layers < 1 || c.layers > 16 || c.width < 1 || c.width > 1024 || c.heads < 1 ||
       c.width % c.heads || (c.width / c.heads) % 2 || c.ffn < 1 || c.ffn > 4096 || c.window < 1 ||
@@ -196,6 +224,11 @@ class Runtime {
   }
   void check_device_error();
   void sync() { HIP_CHECK(hipStreamSynchronize(stream_)); }
+  bool persistent() const { return opt_.backend == ST_BACKEND_PERSISTENT; }
+  void reset_device();
+  void start_worker();
+  void command(int cmd);
+  Mailbox* mailbox() { return reinterpret_cast<Mailbox*>(mailbox_.ptr); }
 
   st_config c_;
   st_options opt_;
@@ -207,6 +240,9 @@ class Runtime {
   hipGraphExec_t graph_exec_ = nullptr;
   DeviceBuffer weights_, keys_, values_, scratch_, tagged_, position_, epoch_, rope_, args_dev_;
   PinnedBuffer host_in_, host_out_;
+  MappedBuffer mailbox_, mapped_in_;
+  uint64_t sequence_ = 0;
+  hipStream_t copy_stream_ = nullptr;
   StepArgs args_{};
   const StepArgs* dargs_ = nullptr;
   std::string probe_;
@@ -224,8 +260,6 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
     throw Error(ST_ERR_INVALID, "Vendor-library backends are not provided by this build");
   if (options.backend < 0 || options.backend > ST_BACKEND_PERSISTENT)
     throw Error(ST_ERR_INVALID, "Unknown backend");
-  if (options.backend == ST_BACKEND_PERSISTENT)
-    throw Error(ST_ERR_INVALID, "Persistent backend not available in this build");
   if (options.weight_dtype == ST_WEIGHTS_BF16 && mixed)
     throw Error(ST_ERR_INVALID, "bfloat16 weight storage applies to FP32 checkpoints only");
   if (options.weight_dtype != ST_WEIGHTS_AS_MODEL && options.weight_dtype != ST_WEIGHTS_BF16)
@@ -243,6 +277,7 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   cus_ = prop.multiProcessorCount;
   HIP_CHECK(hipDeviceGetAttribute(&wall_khz_, hipDeviceAttributeWallClockRate, device));
   HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  HIP_CHECK(hipStreamCreateWithFlags(&copy_stream_, hipStreamNonBlocking));
 
   // ---- shape-derived layout
   StepArgs& a = args_;
@@ -315,6 +350,9 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   a.t_attn = ttake(a.width_p);
   a.t_act = ttake(a.ffn_p);
   a.t_done = ttake(64);
+  a.t_cmd = ttake(64);
+  a.t_in = ttake(a.features_p);
+  a.t_wdone = ttake(kMaxGrid);
   a.t_po = ttake((size_t)c_.heads * nch * dim_);
   a.t_pm = ttake((size_t)c_.heads * nch);
   a.t_ps = ttake((size_t)c_.heads * nch);
@@ -348,29 +386,57 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   legal_blocks_ = dispatch([&](auto P, auto A) { return legal_blocks_t<P.value, A.value>(); });
   grid_ = options.blocks == 0 ? std::min(cus_, kMaxGrid) : options.blocks;
   if (grid_ > kMaxGrid) throw Error(ST_ERR_INVALID, "Requested grid exceeds " + std::to_string(kMaxGrid) + " workgroups");
-  if (options.backend == ST_BACKEND_FUSED && grid_ > legal_blocks_)
+  if ((options.backend == ST_BACKEND_FUSED || options.backend == ST_BACKEND_PERSISTENT) && grid_ > legal_blocks_)
     throw Error(ST_ERR_INVALID,
                 "Requested cooperative grid exceeds actual occupancy limit " + std::to_string(legal_blocks_));
   a.grid = grid_;
+  if (options.backend == ST_BACKEND_PERSISTENT) {
+    mailbox_.alloc(sizeof(Mailbox));
+    mapped_in_.alloc((size_t)c_.features * 4);
+    Mailbox* mb = mailbox();
+    Mailbox* dmb = reinterpret_cast<Mailbox*>(mailbox_.dev);
+    sequence_ = options.initial_sequence;
+    mb->request = sequence_;
+    mb->completion = sequence_;
+    a.mb_request = &dmb->request;
+    a.mb_completion = &dmb->completion;
+    a.mb_exited = &dmb->exited;
+    a.mb_command = &dmb->command;
+    a.mb_score = &dmb->score;
+    a.mb_checksum = &dmb->checksum;
+    a.mb_error = &dmb->error;
+    a.mapped_input = reinterpret_cast<const float*>(mapped_in_.dev);
+    a.idle_ticks = (unsigned long long)(options.idle_seconds * (double)wall_khz_ * 1000.0);
+    a.max_events = options.max_events;
+    a.initial_sequence = options.initial_sequence;
+    a.backoff = options.backoff ? 1 : 0;
+  }
   args_dev_.alloc(sizeof(StepArgs));
   HIP_CHECK(hipMemcpy(args_dev_.ptr, &args_, sizeof(StepArgs), hipMemcpyHostToDevice));
   dargs_ = reinterpret_cast<const StepArgs*>(args_dev_.ptr);
 
-  reset();
+  reset_device();
   if (options.backend == ST_BACKEND_GRAPH) {
     // Warm up outside capture, restore the initial state, then capture the phase sequence.
     launch_phases();
     sync();
-    reset();
+    reset_device();
     HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
     launch_phases();
     HIP_CHECK(hipStreamEndCapture(stream_, &graph_));
     HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
   }
+  if (persistent()) start_worker();
 }
 
 Runtime::~Runtime() {
+  // Join a persistent worker before anything it uses is freed (src/cuda/Runtime.cu:294-299).
+  try {
+    stop();
+  } catch (...) {
+  }
   if (stream_) (void)hipStreamSynchronize(stream_);
+  if (copy_stream_) (void)hipStreamDestroy(copy_stream_);
   if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
   if (graph_) (void)hipGraphDestroy(graph_);
   if (stream_) (void)hipStreamDestroy(stream_);
@@ -532,6 +598,11 @@ void Runtime::check_device_error() {
 float Runtime::step(const float* input) {
   if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
   if (!input) throw Error(ST_ERR_INVALID, "Null input");
+  if (persistent()) {
+    std::memcpy(mapped_in_.ptr, input, (size_t)c_.features * 4);
+    command(kCmdRun);
+    return mailbox()->score;
+  }
   std::memcpy(host_in_.ptr, input, (size_t)c_.features * 4);
   HIP_CHECK(hipMemcpyAsync(args_.scratch + args_.s_input, host_in_.ptr, (size_t)args_.features_p * 4,
                            hipMemcpyHostToDevice, stream_));
@@ -545,39 +616,105 @@ float Runtime::step(const float* input) {
   return out[0];
 }
 
-void Runtime::reset() {
-  if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
+void Runtime::reset_device() {
   hipLaunchKernelGGL(reset_kernel, dim3(std::max(1, std::min(cus_, 1024))), dim3(256), 0, stream_, dargs_);
   HIP_CHECK(hipGetLastError());
   sync();
 }
 
-void Runtime::stop() {
-  if (running_) {
-    sync();
-    running_ = false;
-  }
+void Runtime::reset() {
+  if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
+  if (persistent()) command(kCmdReset);
+  else reset_device();
 }
 
-void Runtime::snapshot(uint64_t* position, float* keys, float* values, float* hidden) {
+// Runtime::stop (src/cuda/Runtime.cu:466-474): a live persistent worker gets STOP, then the
+// stream is joined. Idempotent.
+void Runtime::stop() {
+  if (!running_) return;
+  if (persistent() && !__atomic_load_n(&mailbox()->exited, __ATOMIC_ACQUIRE)) command(kCmdStop);
   sync();
-  if (position) HIP_CHECK(hipMemcpy(position, args_.position, 8, hipMemcpyDeviceToHost));
+  running_ = false;
+}
+
+template <int P, int A>
+static void launch_persistent_t(int grid, const StepArgs* dargs, hipStream_t stream) {
+  if (grid == 1) {
+    hipLaunchKernelGGL((persistent_kernel<P, A>), dim3(1), dim3(kThreads), 0, stream, dargs);
+  } else {
+    void* params[] = {&dargs};
+    HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<void*>(persistent_kernel<P, A>), dim3(grid), dim3(kThreads),
+                                         params, 0, stream));
+  }
+  HIP_CHECK(hipGetLastError());
+}
+
+void Runtime::start_worker() {
+  dispatch([&](auto P, auto A) {
+    launch_persistent_t<P.value, A.value>(grid_, dargs_, stream_);
+    return 0;
+  });
+}
+
+// One command through the mailbox (src/cuda/Runtime.cu:398-428, docs/transport.md:9-16): the
+// input and command are written before the request word is released; the worker's
+// completion word is acquired before the score is read. The last sequence ID is kept for
+// STOP.
+void Runtime::command(int cmd) {
+  if (!running_) throw Error(ST_ERR_STATE, "Persistent runtime is stopped");
+  Mailbox* mb = mailbox();
+  const uint64_t maximum = std::numeric_limits<uint64_t>::max();
+  if (sequence_ == maximum || (sequence_ == maximum - 1 && cmd != kCmdStop))
+    throw Error(ST_ERR_STATE, "Sequence exhausted; create a new runtime before wraparound");
+  if (__atomic_load_n(&mb->exited, __ATOMIC_ACQUIRE)) {
+    sync();
+    running_ = false;
+    throw Error(ST_ERR_STATE, "Persistent worker exited: finite-event or idle budget reached");
+  }
+  mb->command = cmd;
+  __atomic_store_n(&mb->request, ++sequence_, __ATOMIC_RELEASE);
+  const auto start = std::chrono::steady_clock::now();
+  uint64_t polls = 0;
+  while (__atomic_load_n(&mb->completion, __ATOMIC_ACQUIRE) != sequence_) {
+    if (opt_.backoff) std::this_thread::yield();
+    if ((++polls & 0xffff) == 0) {
+      hipError_t status = hipStreamQuery(stream_);
+      if (status != hipErrorNotReady) {
+        HIP_CHECK(status);
+        running_ = false;
+        throw Error(ST_ERR_STATE, "Persistent worker exited before completion");
+      }
+      double waited = std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
+      if (waited > opt_.idle_seconds + 30) throw Error(ST_ERR_STATE, "Persistent response timeout");
+    }
+  }
+  if (mb->error) throw Error(ST_ERR_NUMERIC, "Device watchdog tripped (error bits " + std::to_string(mb->error) + ")");
+}
+
+// Snapshot (src/cuda/Runtime.cu:548-568). Copies run on their own stream: with a persistent
+// worker the runtime's stream is occupied, and the worker's state writes are written through
+// to memory before it completes a command.
+void Runtime::snapshot(uint64_t* position, float* keys, float* values, float* hidden) {
+  if (!persistent() || !running_) sync();
+  auto copy = [&](void* dst, const void* src, size_t bytes) {
+    HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, copy_stream_));
+    HIP_CHECK(hipStreamSynchronize(copy_stream_));
+  };
+  if (position) copy(position, args_.position, 8);
   const size_t n = (size_t)c_.layers * c_.width * c_.window;
   auto download = [&](const void* src, float* dst) {
     if (!dst) return;
     if (prec_ == kMixed) {
       std::vector<uint16_t> h(n);
-      HIP_CHECK(hipMemcpy(h.data(), src, n * 2, hipMemcpyDeviceToHost));
+      copy(h.data(), src, n * 2);
       for (size_t i = 0; i < n; i++) dst[i] = host_half_to_float(h[i]);
     } else {
-      HIP_CHECK(hipMemcpy(dst, src, n * 4, hipMemcpyDeviceToHost));
+      copy(dst, src, n * 4);
     }
   };
   download(args_.keys, keys);
   download(args_.values, values);
-  if (hidden)
-    HIP_CHECK(hipMemcpy(hidden, args_.scratch + args_.s_hidden, (size_t)c_.layers * c_.width * 4,
-                        hipMemcpyDeviceToHost));
+  if (hidden) copy(hidden, args_.scratch + args_.s_hidden, (size_t)c_.layers * c_.width * 4);
 }
 
 template <int P, int A>
@@ -594,6 +731,7 @@ void Runtime::launch_trace_t(const float* events, int count, unsigned long long*
 
 double Runtime::device_trace(const float* inputs, size_t count, double* per_event) {
   if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
+  if (persistent()) throw Error(ST_ERR_INVALID, "Device traces run on launch-per-step backends, not the persistent worker");
   if (!inputs || count == 0 || count > (size_t)std::numeric_limits<int>::max())
     throw Error(ST_ERR_INVALID, "Invalid trace");
   const int fp = args_.features_p;
@@ -648,6 +786,7 @@ double Runtime::device_trace(const float* inputs, size_t count, double* per_even
 // with a HIP event recorded on the runtime's stream after every step.
 double Runtime::device_run(const float* inputs, size_t count, bool reset_first, double* per_event) {
   if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
+  if (persistent()) throw Error(ST_ERR_INVALID, "Device runs use launch-per-step backends, not the persistent worker");
   if (!inputs || count == 0 || count > (size_t)std::numeric_limits<int>::max())
     throw Error(ST_ERR_INVALID, "Invalid trace");
   const int fp = args_.features_p;
@@ -726,11 +865,12 @@ std::string Runtime::info() {
   hipFuncAttributes fa{};
   const void* fn = nullptr;
   std::string name;
-  bool fused = opt_.backend == ST_BACKEND_FUSED;
+  const bool fused = opt_.backend == ST_BACKEND_FUSED, worker = persistent();
   fn = dispatch([&](auto P, auto A) {
-    return fused ? (const void*)fused_kernel<P.value, A.value> : (const void*)phase_kernel<P.value, A.value>;
+    return worker ? (const void*)persistent_kernel<P.value, A.value>
+                  : fused ? (const void*)fused_kernel<P.value, A.value> : (const void*)phase_kernel<P.value, A.value>;
   });
-  name = fused ? "fused_kernel" : "phase_kernel";
+  name = worker ? "persistent_kernel" : fused ? "fused_kernel" : "phase_kernel";
   HIP_CHECK(hipFuncGetAttributes(&fa, fn));
   static const char* backends[] = {"cuda(staged)", "graph", "cublas", "cublas-graph", "fused", "persistent"};
   static const char* precs[] = {"fp32", "mixed", "bf16w"};
@@ -744,8 +884,8 @@ std::string Runtime::info() {
     << ", \"attention_chunk\": " << args_.chunk << ", \"weight_arena_bytes\": " << args_.weight_bytes
     << ", \"matvec_implementation\": \"wave64 16-byte buffer loads, register ring, butterfly reduction\""
     << ", \"attention_implementation\": \"" << (args_.attn_regs ? "register" : "LDS-staged")
-    << " window chunks, last-arriver head combine\""
-    << ", \"transport\": \"pinned-copy-stream-sync\""
+    << " window chunks, tagged partials combined by the chunk-0 wave\""
+    << ", \"transport\": \"" << (worker ? "mapped-mailbox-persistent-worker" : "pinned-copy-stream-sync") << "\""
     << ", \"weights_and_kv_storage\": \""
     << (prec_ == kMixed ? "FP16/FP16" : prec_ == kBf16w ? "BF16/FP32" : "FP32/FP32") << "\"}";
   return o.str();

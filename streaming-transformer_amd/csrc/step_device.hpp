@@ -49,6 +49,9 @@ constexpr int kMaxDim = 1024;
 enum Precision : int { kFp32 = 0, kMixed = 1, kBf16w = 2 };
 enum PhaseKind : int { kInput = 0, kQkv, kAttn, kOut, kGateUp, kDown, kFinal };
 enum ErrorBits : unsigned { kErrPollTimeout = 1u, kErrMailboxTimeout = 2u };
+// Mailbox commands (the reference's Command enum, src/cuda/Primitives.cuh:14), plus the
+// worker's own exit on an exhausted idle budget.
+enum MailboxCommand : int { kCmdRun = 1, kCmdReset = 2, kCmdStop = 3, kCmdPing = 4, kCmdExit = 64 };
 
 // Buffer-resource dword3 for raw buffer access on gfx9 (32-bit data format).
 constexpr int kRsrcWord3 = 0x00020000;
@@ -92,6 +95,20 @@ struct StepArgs {
   const float* rope_freq;          // [dh/2]
   const float* input;              // event source for the INPUT phase (device memory)
   unsigned long long spin_limit;   // poll timeout in wall-clock ticks
+  // persistent backend: mailbox words in coherent pinned host memory (device aliases)
+  unsigned long long* mb_request;
+  unsigned long long* mb_completion;
+  unsigned long long* mb_exited;
+  int* mb_command;
+  float* mb_score;
+  unsigned long long* mb_checksum;
+  unsigned* mb_error;              // device error bits, copied out with each completion
+  const float* mapped_input;       // the host's event buffer
+  unsigned long long idle_ticks;   // idle budget before the worker exits
+  unsigned long long max_events;   // RUN budget (0 = unlimited)
+  unsigned long long initial_sequence;
+  int backoff;                     // sleep between mailbox polls
+  uint32_t t_cmd, t_in, t_wdone;   // tagged: command word, staged event, per-workgroup done
   unsigned long long* stamps;      // optional per-phase wall-clock stamps (workgroup 0)
 };
 

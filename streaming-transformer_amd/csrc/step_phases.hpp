@@ -29,6 +29,7 @@ struct LdsAll {
   float sums[kStreamWaves][kPF][2];      // row sums of units finished in the current ring pass
   float rope[kMaxDim / 2];               // RoPE inverse frequencies
   unsigned done[2];                      // stream waves finished with the phase of this parity
+  int cmd;                               // persistent worker: the current mailbox command
 };
 
 template <int P>
@@ -42,10 +43,11 @@ struct Ctx {
   unsigned base;         // epoch of phase 0 of this step
   bool dead;             // a poll timed out; stop waiting
   const float* input;    // event read by the INPUT phase
+  bool tagged_input;     // the event is the tagged vector t_in (persistent worker)
 
   __device__ __forceinline__ Ctx(const StepArgs& args, LdsAll& l, int grid_index, int grid_size)
       : a(args), lds(l), g(grid_index), grid(grid_size), lane(lane_id()), wave(wave_id()), t(0), valid(0),
-        slot(0), base(0), dead(false), input(args.input) {
+        slot(0), base(0), dead(false), input(args.input), tagged_input(false) {
     wr = make_rsrc(a.weights, a.weight_bytes);
     kr = make_rsrc(a.keys, a.cache_bytes);
     vr = make_rsrc(a.values, a.cache_bytes);
@@ -308,6 +310,10 @@ __device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p, int buf, bool r
     if (mine.count == 0 && !resident) return;
     switch (p.kind) {
       case kInput: {
+        if (c.tagged_input) {
+          poll_vector(c, a.t_in, a.features, a.features_p, c.epoch(0), xs);
+          return;
+        }
         __amdgpu_buffer_rsrc_t ir = make_rsrc(c.input, (uint32_t)a.features_p * 4u);
         for (int i = c.lane * 4; i < a.features_p; i += 256)
           *reinterpret_cast<float4*>(xs + i) = ld16_coherent(ir, (uint32_t)i * 4u);
@@ -920,7 +926,9 @@ __device__ __forceinline__ void compute_final(Ctx<P>& c, const float* xs_buf) {
   float score = wave_sum(acc);
   if (c.lane == 0) {
     c.sstore(a.s_score, score);
-    __hip_atomic_store(a.position, c.t + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // System scope: written through to memory, so a host copy sees it while a persistent
+    // worker is still running.
+    __hip_atomic_store(a.position, c.t + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
@@ -1080,6 +1088,145 @@ __global__ __launch_bounds__(kThreads) void trace_kernel(const StepArgs* __restr
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     stamps[count] = wall_clock64();
     __hip_atomic_store(a.epoch, base0 + (unsigned)count * per_step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Persistent worker's RESET: this workgroup zeroes, with write-through stores, the K/V rows
+// of the attention chunks it reads (items it with it % grid == g, in every layer), so no
+// other XCD's L2 holds a stale copy of them; a grid-strided share of the hidden state; and
+// (workgroup 0) the position.
+template <int P>
+__device__ __forceinline__ void reset_owned(Ctx<P>& c) {
+  const StepArgs& a = c.a;
+  const int nch = (a.window + a.chunk - 1) / a.chunk;
+  const int total = a.heads * nch;
+  for (int it = c.g; it < total; it += c.grid) {
+    const int h = it / nch, ch = it - h * nch;
+    const int row0 = ch * a.chunk;
+    const int rows = a.window - row0 < a.chunk ? a.window - row0 : a.chunk;
+    const uint32_t bytes = (uint32_t)rows * (uint32_t)a.dim * Traits<P>::kKvBytes;  // a multiple of 4
+    for (int l = 0; l < a.layers; l++) {
+      const uint32_t b0 = ((uint32_t)(l * a.heads + h) * (uint32_t)a.window + (uint32_t)row0) * (uint32_t)a.dim *
+                          Traits<P>::kKvBytes;
+      for (uint32_t off = threadIdx.x * 4u; off < bytes; off += kThreads * 4u) {
+        st4_coherent(c.kr, b0 + off, 0.f);
+        st4_coherent(c.vr, b0 + off, 0.f);
+      }
+    }
+  }
+  for (int i = c.g * kThreads + (int)threadIdx.x; i < a.layers * a.width; i += c.grid * kThreads)
+    c.sstore(a.s_hidden + (uint32_t)i, 0.f);
+  if (c.g == 0 && threadIdx.x == 0) __hip_atomic_store(a.position, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Persistent worker (Backend::PERSISTENT): one cooperative launch serves RUN / RESET / PING /
+// STOP commands from a host mailbox, following the reference's persistent_kernel
+// (src/cuda/Runtime.cu:58-122) and its ordering contract (docs/transport.md:9-16):
+//  - workgroup 0's control wave acquires the request word (system scope), stages a RUN's
+//    event into the tagged vector t_in and publishes the command as the tagged word t_cmd
+//    with the command's epoch base; every workgroup polls t_cmd;
+//  - each workgroup reports done (t_wdone[g]) after all of its stores have completed, and
+//    workgroup 0 then writes the score and releases the completion word (system scope);
+//  - the worker exits on STOP, after max_events RUN commands, or when no request arrives
+//    within the idle budget; it then sets the exited word. Every command uses one step's
+//    worth of epochs.
+template <int P, int A>
+__global__ __launch_bounds__(kThreads) void persistent_kernel(const StepArgs* __restrict__ ap) {
+  const StepArgs& a = *ap;
+  __shared__ LdsAll lds;
+  Ctx<P> c(a, lds, (int)blockIdx.x, (int)gridDim.x);
+  c.tagged_input = true;
+  const unsigned base0 = load_epoch(a);
+  const unsigned per_step = (unsigned)ph_final(a) + 2u;
+  unsigned long long t = load_position(a);
+  unsigned long long previous = a.initial_sequence, processed = 0, seq = 0;
+  unsigned k = 0;
+  for (;; k++) {
+    const unsigned base = base0 + k * per_step;
+    c.base = base;
+    if (c.wave == 0) {
+      int cmd = kCmdExit;
+      if (c.g == 0) {
+        unsigned long long got = previous;
+        if (c.lane == 0) {
+          const unsigned long long start = wall_clock64();
+          while (true) {
+            got = __hip_atomic_load(a.mb_request, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (got != previous) {
+              cmd = __hip_atomic_load(a.mb_command, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+              break;
+            }
+            if (wall_clock64() - start >= a.idle_ticks) break;  // idle budget spent: exit
+            if (a.backoff) __builtin_amdgcn_s_sleep(127);
+            else __builtin_amdgcn_s_sleep(2);
+          }
+        }
+        cmd = __shfl(cmd, 0);
+        seq = ((unsigned long long)(unsigned)__shfl((int)(got >> 32), 0) << 32) | (unsigned)__shfl((int)got, 0);
+        if (cmd == kCmdRun)
+          for (int i = c.lane; i < a.features_p; i += 64) c.tstore(a.t_in + (uint32_t)i, base, i < a.features ? a.mapped_input[i] : 0.f);
+        if (c.lane == 0) c.tstore(a.t_cmd, base, __builtin_bit_cast(float, cmd));
+      }
+      // Every workgroup waits for the command (as long as the coordinator may wait, and then
+      // the usual poll limit).
+      const unsigned long long start = wall_clock64();
+      uint2 w;
+      while (true) {
+        w = c.tload(a.t_cmd);
+        if (w.y == base) break;
+        if (wall_clock64() - start > a.idle_ticks + a.spin_limit) {
+          c.timeout();
+          w.x = (unsigned)kCmdExit;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (c.lane == 0) c.lds.cmd = (int)w.x;
+    }
+    lds_barrier();
+    const int cmd = __builtin_amdgcn_readfirstlane(c.lds.cmd);
+    if (cmd == kCmdExit) break;
+    if (cmd == kCmdRun) {
+      c.set_position(t);
+      forward<P, A>(c);
+      t++;
+    } else if (cmd == kCmdReset) {
+      reset_owned(c);
+      t = 0;
+    } else if (cmd == kCmdPing && c.g == 0 && threadIdx.x == 0) {
+      unsigned long long sum = 0;
+      for (int i = 0; i < a.features; i++) sum += __builtin_bit_cast(unsigned, a.mapped_input[i]);
+      __hip_atomic_store(a.mb_checksum, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    // This workgroup's stores are complete: report done for this command.
+    __builtin_amdgcn_s_waitcnt(0);
+    lds_barrier();
+    const unsigned done_ep = base + per_step - 1u;
+    if (threadIdx.x == 0) c.tstore(a.t_wdone + (uint32_t)c.g, done_ep, 0.f);
+    if (c.g == 0 && c.wave == 0) {
+      const unsigned long long start = wall_clock64();
+      while (true) {
+        bool ok = true;
+        for (int i = c.lane; i < c.grid; i += 64) ok = ok && c.tload(a.t_wdone + (uint32_t)i).y == done_ep;
+        if (__all(ok) || c.dead || c.expired(start)) break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (c.lane == 0) {
+        if (cmd == kCmdRun)
+          __hip_atomic_store(a.mb_score, ld4_coherent(c.sr, a.s_score * 4u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(a.mb_error, __hip_atomic_load(a.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(a.mb_completion, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
+    }
+    previous = seq;
+    if (cmd == kCmdRun) processed++;
+    if (cmd == kCmdStop || (a.max_events && processed >= a.max_events)) break;
+    lds_barrier();  // every wave has read lds.cmd before the next command overwrites it
+  }
+  if (c.g == 0 && threadIdx.x == 0) {
+    __hip_atomic_store(a.epoch, base0 + (k + 1u) * per_step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(a.mb_exited, 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
