@@ -164,6 +164,19 @@ def main():
                 n = c.window - 1 + 256
                 _, loop = rt.device_trace(events[:n])
                 extra['device_loop_p50_us'] = nearest_rank(loop[c.window - 1:], 0.5)
+    if not args.quick and backend == Backend.FUSED:
+        # Same service latency through the persistent mailbox worker (no launch per step).
+        popts = RuntimeOptions(backend=Backend.PERSISTENT, blocks=0, weight_dtype=opts.weight_dtype)
+        with Runtime((c, weights, mixed), popts) as rt:
+            for e in events[:fill]:
+                rt.step(e)
+            host = []
+            for e in events[fill:fill + 1024]:
+                s = time.perf_counter()
+                rt.step(e)
+                host.append((time.perf_counter() - s) * 1e6)
+            extra['persistent_service_p50_us'] = nearest_rank(host, 0.5)
+            extra['persistent_service_p99_us'] = nearest_rank(host, 0.99)
 
     achieved = bytes_step / (mean_us * 1e-6) / 1e9
     roofline = {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',

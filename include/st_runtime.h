@@ -58,7 +58,12 @@ typedef struct {
 /* = Stream::RuntimeOptions (include/Runtime.hpp:8-19) plus weight_dtype.
  * blocks: workgroups of 512 threads; 0 selects one per compute unit.
  * vector_matvec and fused_attention are accepted for source compatibility; this
- * backend always uses its wide-load matvec and LDS-staged attention. */
+ * backend always uses its wide-load matvec and LDS-staged attention.
+ * PERSISTENT only: backoff makes the worker and the host spin sleep between polls;
+ * max_events > 0 ends the worker after that many RUN commands (RESET does not count);
+ * initial_sequence is the mailbox's first sequence ID (the last ID is kept for STOP, so
+ * values >= UINT64_MAX - 1 are rejected); idle_seconds ends a worker that receives no
+ * command for that long. A call after the worker has ended fails with ST_ERR_STATE. */
 typedef struct {
   int32_t backend;
   int32_t blocks;
