@@ -294,7 +294,8 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   a.width_p = round_up(c_.width, slab);
   a.ffn_p = round_up(c_.ffn, slab);
   a.features_p = round_up(c_.features, slab);
-  a.chunk = std::min(32, 2048 / dim_);
+  // Window slots per attention item: one K (or V) block of at most kKB 1 KiB slabs in FP32.
+  a.chunk = std::min(4 * kKB, kKB * 256 / dim_);
   if (a.chunk < 1) a.chunk = 1;
   {
     // Register attention: power-of-two head dim with E <= dim <= 64E (E = elements per
@@ -856,8 +857,9 @@ size_t Runtime::phase_times(const float* input, double* us, size_t cap) {
   check_device_error();
   std::vector<unsigned long long> st(n);
   HIP_CHECK(hipMemcpy(st.data(), stamps.ptr, n * 8, hipMemcpyDeviceToHost));
+  // Stamps hold the low 32 bits of the wall clock (the step is far shorter than a wrap).
   for (size_t i = 0; i < n && i < cap; i++)
-    us[i] = st[i] ? (double)(long long)(st[i] - st[0]) * 1000.0 / wall_khz_ : 0.0;
+    us[i] = st[i] ? (double)(int32_t)((uint32_t)st[i] - (uint32_t)st[0]) * 1000.0 / wall_khz_ : 0.0;
   return n;
 }
 

@@ -36,10 +36,20 @@ constexpr int kStreamWaves = kWaves - 1;
 #ifndef STAMD_PF
 #define STAMD_PF 16
 #endif
+#ifndef STAMD_NOPF
+#define STAMD_NOPF 0
+#endif
+#ifndef STAMD_SYNC_PF
+#define STAMD_SYNC_PF 0
+#endif
 constexpr int kPF = STAMD_PF;      // register ring depth (slabs) per stream wave
-constexpr int kKB = 8;             // ring slabs per attention K (or V) block
+constexpr int kKB = kPF >= 16 ? 8 : kPF / 2;  // ring slabs per attention K (or V) block
 static_assert(2 * kKB <= kPF, "an attention item's K and V blocks fit in the ring");
-constexpr int kStamps = 8;         // wall-clock stamps per phase and workgroup (profiling only)
+#ifndef STAMD_POLL_STAMPS
+#define STAMD_POLL_STAMPS 0
+#endif
+constexpr int kStampPhases = 128;  // phases of a step that record stamps (profiling only)
+constexpr int kStamps = STAMD_POLL_STAMPS ? 16 : 8;         // wall-clock stamps per phase and workgroup (profiling only)
 constexpr int kMaxGrid = 1024;     // largest grid accepted
 constexpr int kMaxLayers = 16;
 constexpr int kXs = 4096 + 64;     // LDS activation vector capacity (floats)
@@ -155,16 +165,104 @@ __device__ __forceinline__ float cast(float v) {
   return v;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+
+// Cross-lane reductions without LDS round trips: DPP within rows of 16 lanes (quad_perm
+// [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror, row_ror:8) and the gfx950 permlane
+// swaps across rows (permlane16_swap pairs rows 0/1 and 2/3, permlane32_swap the halves).
+// Every combining step adds (or maxes) a lane's value with its partner's, so the lanes of a
+// group finish with the same bits.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_get(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp_add(float v) { return v + dpp_get<kCtrl>(v); }
+template <int kCtrl>
+__device__ __forceinline__ float dpp_max(float v) { return fmaxf(v, dpp_get<kCtrl>(v)); }
+// Both halves of a swap of v with itself. The vector elements are copied to scalars before
+// any bit cast: __builtin_bit_cast applied to r[1] directly reads element 0.
+template <bool k32>
+__device__ __forceinline__ void swap_halves(float v, float& lo, float& hi) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  unsigned a, b;
+  if constexpr (k32) {
+    auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    a = r[0];
+    b = r[1];
+  } else {
+    auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    a = r[0];
+    b = r[1];
+  }
+  lo = __builtin_bit_cast(float, a);
+  hi = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float pair16_add(float v) {
+  float a, b;
+  swap_halves<false>(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float pair32_add(float v) {
+  float a, b;
+  swap_halves<true>(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float pair16_max(float v) {
+  float a, b;
+  swap_halves<false>(v, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float pair32_max(float v) {
+  float a, b;
+  swap_halves<true>(v, a, b);
+  return fmaxf(a, b);
+}
+// Sum over aligned groups of `group` lanes (a power of two up to 64), in every lane.
+__device__ __forceinline__ float group_sum(float v, int group) {
+  if (group >= 2) v = dpp_add<0xB1>(v);
+  if (group >= 4) v = dpp_add<0x4E>(v);
+  if (group >= 8) v = dpp_add<0x141>(v);
+  if (group >= 16) v = dpp_add<0x140>(v);
+  if (group >= 32) v = pair16_add(v);
+  if (group >= 64) v = pair32_add(v);
   return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+// Sum over the lanes that share lane % group (group a power of two up to 64).
+__device__ __forceinline__ float column_sum(float v, int group) {
+  for (int o = group; o < 8; o <<= 1) v += __shfl_xor(v, o);
+  if (group <= 8) v = dpp_add<0x128>(v);  // row_ror:8 pairs lane i with lane i ^ 8
+  if (group <= 16) v = pair16_add(v);
+  if (group <= 32) v = pair32_add(v);
   return v;
 }
+__device__ __forceinline__ float wave_total(float v) {
+  v = dpp_add<0xB1>(v);
+  v = dpp_add<0x4E>(v);
+  v = dpp_add<0x141>(v);
+  v = dpp_add<0x140>(v);
+  v = pair16_add(v);
+  return pair32_add(v);
+}
+__device__ __forceinline__ float wave_top(float v) {
+  v = dpp_max<0xB1>(v);
+  v = dpp_max<0x4E>(v);
+  v = dpp_max<0x141>(v);
+  v = dpp_max<0x140>(v);
+  v = pair16_max(v);
+  return pair32_max(v);
+}
+
+// LDS-typed pointers: stores through them are ds_write, never flat (a flat access to LDS
+// goes through the vector memory pipeline and waits behind outstanding global loads).
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) float lds_float;
+typedef __attribute__((address_space(3))) v2f lds_v2f;
+typedef __attribute__((address_space(3))) v4f lds_v4f;
+__device__ __forceinline__ lds_float* to_lds(float* p) { return (lds_float*)p; }
+// Store two (four) consecutive floats to LDS at p (8- or 16-byte aligned).
+__device__ __forceinline__ void lds_store2(float* p, float2 v) { *(lds_v2f*)p = v2f{v.x, v.y}; }
+__device__ __forceinline__ void lds_store4(float* p, float4 v) { *(lds_v4f*)p = v4f{v.x, v.y, v.z, v.w}; }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }

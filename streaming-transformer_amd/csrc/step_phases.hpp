@@ -29,7 +29,9 @@ struct LdsAll {
   float sums[kStreamWaves][kPF][2];      // row sums of units finished in the current ring pass
   float rope[kMaxDim / 2];               // RoPE inverse frequencies
   unsigned done[2];                      // stream waves finished with the phase of this parity
+  unsigned issued;                       // stream-wave phases whose results are issued, this forward
   int cmd;                               // persistent worker: the current mailbox command
+  unsigned stamps[kStampPhases][kStamps];  // profiling: low 32 bits of the wall clock
 };
 
 template <int P>
@@ -44,6 +46,9 @@ struct Ctx {
   bool dead;             // a poll timed out; stop waiting
   const float* input;    // event read by the INPUT phase
   bool tagged_input;     // the event is the tagged vector t_in (persistent worker)
+#if STAMD_POLL_STAMPS
+  int pph = -1;  // phase whose staging stamps the polls record (control wave)
+#endif
 
   __device__ __forceinline__ Ctx(const StepArgs& args, LdsAll& l, int grid_index, int grid_size)
       : a(args), lds(l), g(grid_index), grid(grid_size), lane(lane_id()), wave(wave_id()), t(0), valid(0),
@@ -103,20 +108,25 @@ __device__ __forceinline__ int ph_final(const StepArgs& a) { return 1 + 5 * a.la
 // Phase that last wrote x before `layer`'s QKV phase.
 __device__ __forceinline__ int ph_x_before(int layer) { return layer == 0 ? 0 : ph_index(kDown, layer - 1); }
 
-// Profiling stamp k of phase p for this workgroup (lane 0 of the calling wave), when the
-// launch carries a stamp buffer. Slots: 0 phase start, 1 stream wave 1 done, 2 all stream
-// waves done, 3 next phase's inputs staged, 4-6 progress of stream wave 1 within the phase,
-// 7 stream wave 1 has issued the next phase's prefetch.
-__device__ __forceinline__ void put_stamp(unsigned long long* base, size_t index) {
-  // A global (not flat) store: it counts only against vmcnt, so LDS waits never wait for it.
-  typedef __attribute__((address_space(1))) unsigned long long gu64;
-  ((gu64*)base)[index] = wall_clock64();
+// Profiling stamp k of phase `ph` for this workgroup, when the launch carries a stamp buffer.
+// Slots: 0 phase start, 1 stream wave 1 done, 2 all stream waves done, 3 next phase's inputs
+// staged, 4-6 progress of stream wave 1 within the phase, 7 stream wave 1 has issued the
+// next phase's prefetch. Stamps go to LDS and are written out once, after the step, so that
+// recording them puts no stores into the memory pipeline the step is using.
+template <int P>
+__device__ __forceinline__ void lstamp(Ctx<P>& c, int ph, int k) {
+  if (c.a.stamps && ph < kStampPhases) c.lds.stamps[ph][k] = (unsigned)wall_clock64();
 }
 
 template <int P>
 __device__ __forceinline__ void stamp(Ctx<P>& c, Phase p, int k) {
-  if (c.a.stamps && c.lane == 0)
-    put_stamp(c.a.stamps, (size_t)kStamps * ((size_t)ph_index(p.kind, p.layer) * (size_t)c.grid + (size_t)c.g) + (size_t)k);
+  if (c.lane == 0) lstamp(c, ph_index(p.kind, p.layer), k);
+}
+
+// A global (not flat) 64-bit store: it counts only against vmcnt.
+__device__ __forceinline__ void put_global(unsigned long long* base, size_t index, unsigned long long v) {
+  typedef __attribute__((address_space(1))) unsigned long long gu64;
+  ((gu64*)base)[index] = v;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -125,12 +135,14 @@ __device__ __forceinline__ void stamp(Ctx<P>& c, Phase p, int k) {
 constexpr int kPollSleep = 2;  // s_sleep units (64 clocks each) between failed polls
 
 // Wait until elements [2*p0, 2*(p0+np)) of tagged vector `tv` carry epoch `ep` (elements at or
-// beyond `n` are padding and are not checked), then write their values (0 for padding) to
-// dst[0 ..). One wave; NP 16-byte pieces per lane per pass.
+// beyond `n` are padding and are not checked); the pieces stay in buf. One wave; NP 16-byte
+// pieces (2 elements) per lane per pass: lane l holds pieces l, l + 64, ...
 template <int P, int NP>
-__device__ __forceinline__ void poll_pieces(Ctx<P>& c, uint32_t tv, int n, int p0, int np, unsigned ep, float* dst) {
-  uint4 buf[NP];
+__device__ __forceinline__ void poll_regs(Ctx<P>& c, uint32_t tv, int n, int p0, int np, unsigned ep, uint4 (&buf)[NP]) {
   unsigned long long start = wall_clock64();
+#if STAMD_POLL_STAMPS
+  bool first_pass = p0 == 0;
+#endif
   while (true) {
 #pragma unroll
     for (int k = 0; k < NP; k++) {
@@ -147,6 +159,13 @@ __device__ __forceinline__ void poll_pieces(Ctx<P>& c, uint32_t tv, int n, int p
       bool in = pc < np;
       ok = ok && (!in || ((e0 >= n || buf[k].y == ep) && (e0 + 1 >= n || buf[k].w == ep)));
     }
+#if STAMD_POLL_STAMPS
+    if (c.pph >= 0 && c.lane == 0) {
+      if (first_pass) lstamp(c, c.pph, 8);
+      lstamp(c, c.pph, 9);
+    }
+    first_pass = false;
+#endif
     if (__all(ok) || c.dead) break;
     if (wall_clock64() - start > c.a.spin_limit) {
       c.timeout();
@@ -154,14 +173,25 @@ __device__ __forceinline__ void poll_pieces(Ctx<P>& c, uint32_t tv, int n, int p
     }
     __builtin_amdgcn_s_sleep(kPollSleep);
   }
+#if STAMD_POLL_STAMPS
+  if (c.pph >= 0 && c.lane == 0) lstamp(c, c.pph, 10);
+#endif
+}
+
+// Value pair of piece k (0 for padding at or beyond n).
+__device__ __forceinline__ float2 piece_values(uint4 b, int e0, int n) {
+  return make_float2(e0 < n ? __builtin_bit_cast(float, b.x) : 0.f, e0 + 1 < n ? __builtin_bit_cast(float, b.z) : 0.f);
+}
+
+// poll_regs, then write the values (0 for padding) to dst[0 ..) in LDS.
+template <int P, int NP>
+__device__ __forceinline__ void poll_pieces(Ctx<P>& c, uint32_t tv, int n, int p0, int np, unsigned ep, float* dst) {
+  uint4 buf[NP];
+  poll_regs<P, NP>(c, tv, n, p0, np, ep, buf);
 #pragma unroll
   for (int k = 0; k < NP; k++) {
     int pc = c.lane + 64 * k;
-    int e0 = 2 * (p0 + pc);
-    if (pc < np) {
-      dst[2 * pc] = e0 < n ? __builtin_bit_cast(float, buf[k].x) : 0.f;
-      dst[2 * pc + 1] = e0 + 1 < n ? __builtin_bit_cast(float, buf[k].z) : 0.f;
-    }
+    if (pc < np) lds_store2(dst + 2 * pc, piece_values(buf[k], 2 * (p0 + pc), n));
   }
 }
 
@@ -202,10 +232,11 @@ __device__ __forceinline__ void poll_range(Ctx<P>& c, uint32_t tv, int first, in
       }
       __builtin_amdgcn_s_sleep(kPollSleep);
     }
+    lds_float* d = to_lds(dst);
 #pragma unroll
     for (int k = 0; k < NE; k++) {
       int e = e0 + c.lane + 64 * k;
-      if (e < count) dst[e] = __builtin_bit_cast(float, buf[k].x);
+      if (e < count) d[e] = __builtin_bit_cast(float, buf[k].x);
     }
   }
 }
@@ -213,49 +244,51 @@ __device__ __forceinline__ void poll_range(Ctx<P>& c, uint32_t tv, int first, in
 // ---------------------------------------------------------------------------------------------
 // control wave: stage phase inputs into LDS
 
-// RMSNorm in place over v[0 .. width) (src/cuda/Primitives.cuh:122-135):
-// s = 1/sqrt(sum(v^2)/d + eps), v = cast(v * s * w).
-constexpr int kNormK = kMaxDim / 64;  // norm weights per lane
+// Pieces per lane of a staged vector of up to kMaxDim elements.
+constexpr int kStageNP = kMaxDim / 128;
 
-// Issue the loads of a norm weight vector (lane i holds elements i, i + 64, ...).
+// Norm weights in the piece layout of poll_regs: lane l, piece k holds elements
+// 2(l + 64k) and 2(l + 64k) + 1 (clamped; the padding they multiply is 0).
 template <int P>
-__device__ __forceinline__ void load_norm(Ctx<P>& c, uint32_t w_off, float (&w)[kNormK]) {
+__device__ __forceinline__ void load_norm(Ctx<P>& c, uint32_t w_off, float2 (&w)[kStageNP]) {
   const int d = c.a.width;
 #pragma unroll
-  for (int k = 0; k < kNormK; k++) {
-    int i = c.lane + 64 * k;
-    w[k] = load_weight_scalar<P>(c.wr, w_off, i < d ? i : d - 1);
+  for (int k = 0; k < kStageNP; k++) {
+    int e0 = 2 * (c.lane + 64 * k);
+    w[k] = make_float2(load_weight_scalar<P>(c.wr, w_off, e0 < d ? e0 : d - 1),
+                       load_weight_scalar<P>(c.wr, w_off, e0 + 1 < d ? e0 + 1 : d - 1));
   }
 }
 
-// RMSNorm in place over v[0 .. width) (src/cuda/Primitives.cuh:122-135):
-// s = 1/sqrt(sum(v^2)/d + eps), v = cast(v * s * w).
+// Stage one tagged vector of n elements (np pieces, np <= 64 * kStageNP) from registers:
+// the raw values to `raw` (when not null) and to `xs`, RMS-normalized when `norm`
+// (src/cuda/Primitives.cuh:122-135: s = 1/sqrt(sum(v^2)/d + eps), v = cast(v * s * w)).
 template <int P>
-__device__ __forceinline__ void norm_in_lds(Ctx<P>& c, float* v, const float (&w)[kNormK]) {
-  const int d = c.a.width;
+__device__ __forceinline__ void stage_vector(Ctx<P>& c, uint32_t tv, int n, int np, unsigned ep, float* xs, float* raw,
+                                             bool norm, const float2 (&w)[kStageNP]) {
+  uint4 buf[kStageNP];
+  poll_regs<P, kStageNP>(c, tv, n, 0, np, ep, buf);
+  float2 x[kStageNP];
   float sum = 0.f;
 #pragma unroll
-  for (int k = 0; k < kNormK; k++) {
-    int i = c.lane + 64 * k;
-    if (i < d) sum += v[i] * v[i];
+  for (int k = 0; k < kStageNP; k++) {
+    int pc = c.lane + 64 * k;
+    x[k] = pc < np ? piece_values(buf[k], 2 * pc, n) : make_float2(0.f, 0.f);
+    sum += x[k].x * x[k].x + x[k].y * x[k].y;
   }
-  sum = wave_sum(sum);
-  const float scale = 1.0f / sqrtf(sum / (float)d + c.a.epsilon);
+  if (raw) {
 #pragma unroll
-  for (int k = 0; k < kNormK; k++) {
-    int i = c.lane + 64 * k;
-    if (i < d) v[i] = cast<P>(v[i] * scale * w[k]);
+    for (int k = 0; k < kStageNP; k++)
+      if (c.lane + 64 * k < np) lds_store2(raw + 2 * (c.lane + 64 * k), x[k]);
   }
-}
-
-// Copy v[0 .. width) to dst (the raw x kept for a later residual).
-template <int P>
-__device__ __forceinline__ void keep_raw(Ctx<P>& c, const float* v, float* dst) {
+  if (norm) {
+    const float scale = 1.0f / sqrtf(wave_total(sum) / (float)c.a.width + c.a.epsilon);
 #pragma unroll
-  for (int k = 0; k < kNormK; k++) {
-    int i = c.lane + 64 * k;
-    if (i < c.a.width) dst[i] = v[i];
+    for (int k = 0; k < kStageNP; k++) x[k] = make_float2(cast<P>(x[k].x * scale * w[k].x), cast<P>(x[k].y * scale * w[k].y));
   }
+#pragma unroll
+  for (int k = 0; k < kStageNP; k++)
+    if (c.lane + 64 * k < np) lds_store2(xs + 2 * (c.lane + 64 * k), x[k]);
 }
 
 // Units of a matvec phase owned by workgroup g: [first, first + count).
@@ -289,7 +322,7 @@ __device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p, int buf, bool r
   float* raw = nullptr;
   float* own_dst = nullptr;
   bool norm = false;
-  float nw[kNormK];
+  float2 nw[kStageNP];
   Own own{0, 0};
   if (p.kind == kAttn) {
     if constexpr (A == 1) return;
@@ -316,7 +349,7 @@ __device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p, int buf, bool r
         }
         __amdgpu_buffer_rsrc_t ir = make_rsrc(c.input, (uint32_t)a.features_p * 4u);
         for (int i = c.lane * 4; i < a.features_p; i += 256)
-          *reinterpret_cast<float4*>(xs + i) = ld16_coherent(ir, (uint32_t)i * 4u);
+          lds_store4(xs + i, ld16_coherent(ir, (uint32_t)i * 4u));
         return;
       }
       case kQkv:
@@ -354,10 +387,16 @@ __device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p, int buf, bool r
         break;
     }
   }
-  for (int v = 0; v < nvec; v++) poll_vector(c, vec[v], n, n_p, ep, dst[v]);
+  if (nvec == 1 && n_p / 2 <= 64 * kStageNP) {
+    stage_vector(c, vec[0], n, n_p / 2, ep, dst[0], raw, norm, nw);
+  } else {
+    // Wider vectors and the attention q/k/v carry no norm or raw copy.
+    for (int v = 0; v < nvec; v++) poll_vector(c, vec[v], n, n_p, ep, dst[v]);
+  }
+#if STAMD_POLL_STAMPS
+  if (c.pph >= 0 && c.lane == 0) lstamp(c, c.pph, 11);
+#endif
   if (own.count) poll_range(c, a.t_x, own.first, own.count, ep_own, own_dst);
-  if (raw) keep_raw(c, xs, raw);
-  if (norm) norm_in_lds(c, xs, nw);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -521,8 +560,8 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* 
           s = 0;
           if (++ru == m.unit) {
             ru = 0;
-            float s0 = wave_sum(acc0);
-            float s1 = m.unit == 2 ? wave_sum(acc1) : 0.f;
+            float s0 = wave_total(acc0);
+            float s1 = m.unit == 2 ? wave_total(acc1) : 0.f;
             if (c.lane == 0) {
               sums[finished][0] = s0;
               sums[finished][1] = s1;
@@ -569,6 +608,37 @@ __device__ __forceinline__ void combine_head(Ctx<P>& c, int layer, int h, int nc
   const int dim = a.dim;
   const unsigned ep = c.epoch(ph_index(kAttn, layer));
   const uint32_t item0 = (uint32_t)(h * nch);
+  if (nactive <= 16 && dim <= 64) {
+    // One pass: lane c polls (m_c, s_c) and lane i polls o_c[i] of every chunk.
+    const int cl = c.lane < nactive ? c.lane : nactive - 1;
+    const int il = c.lane < dim ? c.lane : dim - 1;
+    uint2 pm, ps, po[16];
+    unsigned long long start = wall_clock64();
+    while (true) {
+      pm = c.tload(a.t_pm + item0 + (uint32_t)cl);
+      ps = c.tload(a.t_ps + item0 + (uint32_t)cl);
+#pragma unroll
+      for (int k = 0; k < 16; k++) {
+        int cc = k < nactive ? k : nactive - 1;
+        po[k] = c.tload(a.t_po + (item0 + (uint32_t)cc) * (uint32_t)dim + (uint32_t)il);
+      }
+      bool ok = pm.y == ep && ps.y == ep;
+#pragma unroll
+      for (int k = 0; k < 16; k++) ok = ok && po[k].y == ep;
+      if (__all(ok) || c.dead || c.expired(start)) break;
+      __builtin_amdgcn_s_sleep(kPollSleep);
+    }
+    const float mc = __builtin_bit_cast(float, pm.x), sc = __builtin_bit_cast(float, ps.x);
+    const float big = wave_top(c.lane < nactive ? mc : -INFINITY);
+    const float e = c.lane < nactive ? expf(mc - big) : 0.f;
+    const float denom = wave_total(sc * e);
+    float o = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+      if (k < nactive) o += __builtin_bit_cast(float, po[k].x) * lane_value(e, k);
+    if (c.lane < dim) c.tstore(a.t_attn + h * dim + c.lane, ep, cast<P>(o / denom));
+    return;
+  }
   if (nactive <= 64 && dim <= 64) {
     // Lane c polls (m_c, s_c); then lane i reads o_c[i] of the chunks in groups of 8.
     const int cl = c.lane < nactive ? c.lane : nactive - 1;
@@ -582,9 +652,9 @@ __device__ __forceinline__ void combine_head(Ctx<P>& c, int layer, int h, int nc
       __builtin_amdgcn_s_sleep(kPollSleep);
     }
     const float mc = __builtin_bit_cast(float, pm.x), sc = __builtin_bit_cast(float, ps.x);
-    const float big = wave_max(c.lane < nactive ? mc : -INFINITY);
+    const float big = wave_top(c.lane < nactive ? mc : -INFINITY);
     const float e = c.lane < nactive ? expf(mc - big) : 0.f;
-    const float denom = wave_sum(sc * e);
+    const float denom = wave_total(sc * e);
     float o = 0.f;
     for (int k0 = 0; k0 < nactive; k0 += 8) {
       uint2 po[8];
@@ -625,7 +695,7 @@ __device__ __forceinline__ void combine_head(Ctx<P>& c, int layer, int h, int nc
     int cc = c0 + c.lane;
     if (cc < nactive) big = fmaxf(big, __builtin_bit_cast(float, c.tload(a.t_pm + item0 + (uint32_t)cc).x));
   }
-  big = wave_max(big);
+  big = wave_top(big);
   float denom = 0.f;
   for (int c0 = 0; c0 < nactive; c0 += 64) {
     int cc = c0 + c.lane;
@@ -635,7 +705,7 @@ __device__ __forceinline__ void combine_head(Ctx<P>& c, int layer, int h, int nc
       denom += sc * expf(mc - big);
     }
   }
-  denom = wave_sum(denom);
+  denom = wave_total(denom);
   for (int i = c.lane; i < dim; i += 64) {
     float o = 0.f;
     for (int cc = 0; cc < nactive; cc++) {
@@ -777,11 +847,11 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
       float dot = 0.f;
 #pragma unroll
       for (int e = 0; e < E; e++) dot += q[e] * (cur ? kc[e] : k[e]);
-      for (int o = group >> 1; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
+      dot = group_sum(dot, group);
       logit[j] = live ? dot / div : -INFINITY;
       mx = fmaxf(mx, logit[j]);
     }
-    mx = wave_max(mx);
+    mx = wave_top(mx);
     float psum = 0.f;
     float out[E];
 #pragma unroll
@@ -797,10 +867,10 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
 #pragma unroll
       for (int e = 0; e < E; e++) out[e] += pr * (cur ? vc[e] : v[e]);
     }
-    float total = wave_sum((c.lane & (group - 1)) == 0 ? psum : 0.f);
+    float total = wave_total((c.lane & (group - 1)) == 0 ? psum : 0.f);
 #pragma unroll
     for (int e = 0; e < E; e++)
-      for (int o = 32; o >= group; o >>= 1) out[e] += __shfl_xor(out[e], o);
+      out[e] = column_sum(out[e], group);
     const unsigned ep = c.epoch(ph_index(kAttn, p.layer));
     if (c.lane < group) {
       const uint32_t ob = (uint32_t)it * (uint32_t)dim + (uint32_t)col0;
@@ -887,9 +957,9 @@ __device__ __forceinline__ void compute_attn_lds(Ctx<P>& c, Phase p, uint4 (&rin
       for (int i = 0; i < dim; i++) dot += q[i] * krow[i];
       logit = dot / div;
     }
-    float mx = wave_max(logit);
+    float mx = wave_top(logit);
     float pr = c.lane < rows ? expf(logit - mx) : 0.f;
-    float total = wave_sum(pr);
+    float total = wave_total(pr);
     probs[c.lane] = pr;
     __builtin_amdgcn_wave_barrier();
     block_to_lds<P>(c, ring + kKB, w.kchunks, stage);
@@ -923,7 +993,7 @@ __device__ __forceinline__ void compute_final(Ctx<P>& c, const float* xs_buf) {
 #pragma unroll
   for (int s = 0; s < kMaxDim * 4 / 1024; s++)
     if (s < slabs) acc += chunk_dot<P>(wv[s], xs_buf + (s * 64 + c.lane) * Traits<P>::kEpc);
-  float score = wave_sum(acc);
+  float score = wave_total(acc);
   if (c.lane == 0) {
     c.sstore(a.s_score, score);
     // System scope: written through to memory, so a host copy sees it while a persistent
@@ -982,18 +1052,16 @@ __global__ __launch_bounds__(kThreads) void phase_kernel(const StepArgs* __restr
 template <int P, int A>
 __device__ __forceinline__ void control_loop(Ctx<P>& c, int nph) {
   const StepArgs& a = c.a;
-  // Optional wall-clock stamps (slots as in stamp()); the step end follows the last phase.
+  // Optional wall-clock stamps (slots as in lstamp()); the step end follows the last phase.
   const bool stamps = a.stamps && threadIdx.x == 0;
-  unsigned long long* st = a.stamps + kStamps * c.g;
-  const int sst = kStamps * c.grid;
   stage_inputs<P, A>(c, phase_of(a, 0), 0, true);
   for (int ph = 0; ph < nph; ph++) {
     lds_barrier();
-    if (stamps) put_stamp(st, sst * ph);
+    if (stamps) lstamp(c, ph, 0);
     Phase p = phase_of(a, ph);
     if (p.kind == kFinal) {
       if (c.g == 0) compute_final(c, c.lds.xs[ph & 1]);
-      if (stamps && c.g == 0) put_stamp(a.stamps, sst * nph);
+      if (stamps && c.g == 0) put_global(a.stamps, (size_t)kStamps * c.grid * nph, wall_clock64());
       break;
     }
     // Start polling for the next phase's inputs only once this workgroup's own part of
@@ -1002,9 +1070,12 @@ __device__ __forceinline__ void control_loop(Ctx<P>& c, int nph) {
     while (__hip_atomic_load(&c.lds.done[ph & 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)kStreamWaves)
       __builtin_amdgcn_s_sleep(1);
     if (c.lane == 0) __hip_atomic_store(&c.lds.done[ph & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (stamps) put_stamp(st, sst * ph + 2);
+    if (stamps) lstamp(c, ph, 2);
+#if STAMD_POLL_STAMPS
+    c.pph = a.stamps ? ph : -1;
+#endif
     stage_inputs<P, A>(c, phase_of(a, ph + 1), (ph + 1) & 1, true);
-    if (stamps) put_stamp(st, sst * ph + 3);
+    if (stamps) lstamp(c, ph, 3);
   }
 }
 
@@ -1014,21 +1085,31 @@ template <int P, int A>
 __device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
   const StepArgs& a = c.a;
   const bool stamps = a.stamps && c.wave == 1 && c.lane == 0;
-  unsigned long long* st = a.stamps + kStamps * c.g;
-  const int sst = kStamps * c.grid;
   uint4 ring[kPF];
+#if !STAMD_NOPF
   prefetch(c, phase_of(a, 0), ring);
+#endif
   for (int ph = 0; ph < nph; ph++) {
     lds_barrier();
     Phase p = phase_of(a, ph);
     if (p.kind == kFinal) break;
+#if STAMD_NOPF
+    prefetch(c, p, ring);
+#endif
     compute<P, A>(c, p, ph & 1, ring);
-    if (stamps) put_stamp(st, sst * ph + 1);
+    if (stamps) lstamp(c, ph, 1);
     // Signal before issuing the next phase's prefetch: the issue itself can stall on a
     // full memory pipeline, and the control wave can stage meanwhile.
     if (c.lane == 0) __hip_atomic_fetch_add(&c.lds.done[ph & 1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#if STAMD_SYNC_PF
+    if (c.lane == 0) __hip_atomic_fetch_add(&c.lds.issued, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    while (__hip_atomic_load(&c.lds.issued, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)(kStreamWaves * (ph + 1)))
+      __builtin_amdgcn_s_sleep(1);
+#endif
+#if !STAMD_NOPF
     prefetch(c, phase_of(a, ph + 1), ring);
-    if (stamps) put_stamp(st, sst * ph + 7);
+#endif
+    if (stamps) lstamp(c, ph, 7);
   }
 }
 
@@ -1040,10 +1121,20 @@ __device__ __forceinline__ void forward(Ctx<P>& c) {
   if (threadIdx.x == 0) {
     c.lds.done[0] = 0;
     c.lds.done[1] = 0;
+    c.lds.issued = 0;
   }
   for (int i = threadIdx.x; i < a.dim / 2; i += kThreads) c.lds.rope[i] = a.rope_freq[i];
+  const int nst = (nph < kStampPhases ? nph : kStampPhases) * kStamps;
+  if (a.stamps)
+    for (int i = threadIdx.x; i < nst; i += kThreads) (&c.lds.stamps[0][0])[i] = 0u;
   if (c.wave == 0) control_loop<P, A>(c, nph);
   else stream_loop<P, A>(c, nph);
+  if (a.stamps) {
+    lds_barrier();
+    for (int i = threadIdx.x; i < nst; i += kThreads)
+      put_global(a.stamps, (size_t)kStamps * ((size_t)(i / kStamps) * c.grid + c.g) + i % kStamps,
+                 (&c.lds.stamps[0][0])[i]);
+  }
 }
 
 // One step per launch (fused backend). `event` overrides the INPUT source when not null.
