@@ -34,7 +34,10 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kStreamWaves = kWaves - 1;
 #ifndef STAMD_PF
-#define STAMD_PF 16
+#define STAMD_PF 8
+#endif
+#ifndef STAMD_PACE
+#define STAMD_PACE 0
 #endif
 #ifndef STAMD_NOPF
 #define STAMD_NOPF 0
@@ -263,6 +266,7 @@ __device__ __forceinline__ lds_float* to_lds(float* p) { return (lds_float*)p; }
 // Store two (four) consecutive floats to LDS at p (8- or 16-byte aligned).
 __device__ __forceinline__ void lds_store2(float* p, float2 v) { *(lds_v2f*)p = v2f{v.x, v.y}; }
 __device__ __forceinline__ void lds_store4(float* p, float4 v) { *(lds_v4f*)p = v4f{v.x, v.y, v.z, v.w}; }
+
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }

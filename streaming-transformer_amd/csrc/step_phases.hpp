@@ -143,14 +143,13 @@ __device__ __forceinline__ void poll_regs(Ctx<P>& c, uint32_t tv, int n, int p0,
 #if STAMD_POLL_STAMPS
   bool first_pass = p0 == 0;
 #endif
+  // One lane offset; piece k adds k * 1 KiB as the scalar offset. Pieces past np read
+  // whatever follows in the tagged arena (or 0 past its end) and are ignored.
+  const uint32_t voff = (tv + 2u * (uint32_t)(p0 + c.lane)) * 8u;
   while (true) {
 #pragma unroll
-    for (int k = 0; k < NP; k++) {
-      int pc = c.lane + 64 * k;
-      int pcl = pc < np ? pc : np - 1;
-      buf[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             c.tr, (int)((tv + 2u * (uint32_t)(p0 + pcl)) * 8u), 0, kSc1));
-    }
+    for (int k = 0; k < NP; k++)
+      buf[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(c.tr, (int)voff, 1024 * k, kSc1));
     bool ok = true;
 #pragma unroll
     for (int k = 0; k < NP; k++) {
@@ -426,6 +425,9 @@ __device__ __forceinline__ void prefetch_matvec(Ctx<P>& c, const WaveWork& w, ui
   for (int j = 0; j < kPF; j++) {
     ring[j] = ld16(c.wr, (j < w.slabs ? cur : last).offset(c.lane));
     cur.advance(w);
+#if STAMD_PACE
+    __builtin_amdgcn_s_sleep(STAMD_PACE);
+#endif
   }
 }
 
@@ -602,29 +604,31 @@ __device__ __forceinline__ float lane_value(float v, int k) {
 // of its own items, so no wave waits on work queued behind its own wait), in chunk order:
 //   attn = sum_c o_c exp(m_c - M) / sum_c s_c exp(m_c - M),  M = max_c m_c,
 // then publish attn_h. Polls the tagged partials.
+constexpr int kCombineOne = 32;  // chunks a head combines in one polling pass
+
 template <int P>
 __device__ __forceinline__ void combine_head(Ctx<P>& c, int layer, int h, int nch, int nactive) {
   const StepArgs& a = c.a;
   const int dim = a.dim;
   const unsigned ep = c.epoch(ph_index(kAttn, layer));
   const uint32_t item0 = (uint32_t)(h * nch);
-  if (nactive <= 16 && dim <= 64) {
+  if (nactive <= kCombineOne && dim <= 64) {
     // One pass: lane c polls (m_c, s_c) and lane i polls o_c[i] of every chunk.
     const int cl = c.lane < nactive ? c.lane : nactive - 1;
     const int il = c.lane < dim ? c.lane : dim - 1;
-    uint2 pm, ps, po[16];
+    uint2 pm, ps, po[kCombineOne];
     unsigned long long start = wall_clock64();
     while (true) {
       pm = c.tload(a.t_pm + item0 + (uint32_t)cl);
       ps = c.tload(a.t_ps + item0 + (uint32_t)cl);
 #pragma unroll
-      for (int k = 0; k < 16; k++) {
+      for (int k = 0; k < kCombineOne; k++) {
         int cc = k < nactive ? k : nactive - 1;
         po[k] = c.tload(a.t_po + (item0 + (uint32_t)cc) * (uint32_t)dim + (uint32_t)il);
       }
       bool ok = pm.y == ep && ps.y == ep;
 #pragma unroll
-      for (int k = 0; k < 16; k++) ok = ok && po[k].y == ep;
+      for (int k = 0; k < kCombineOne; k++) ok = ok && po[k].y == ep;
       if (__all(ok) || c.dead || c.expired(start)) break;
       __builtin_amdgcn_s_sleep(kPollSleep);
     }
@@ -634,7 +638,7 @@ __device__ __forceinline__ void combine_head(Ctx<P>& c, int layer, int h, int nc
     const float denom = wave_total(sc * e);
     float o = 0.f;
 #pragma unroll
-    for (int k = 0; k < 16; k++)
+    for (int k = 0; k < kCombineOne; k++)
       if (k < nactive) o += __builtin_bit_cast(float, po[k].x) * lane_value(e, k);
     if (c.lane < dim) c.tstore(a.t_attn + h * dim + c.lane, ep, cast<P>(o / denom));
     return;
