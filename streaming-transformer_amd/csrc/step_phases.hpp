@@ -30,6 +30,7 @@ struct LdsAll {
   float rope[kMaxDim / 2];               // RoPE inverse frequencies
   unsigned done[2];                      // stream waves finished with the phase of this parity
   unsigned issued;                       // stream-wave phases whose results are issued, this forward
+  unsigned helped;                       // epoch of the wide vector whose odd chunks the helper staged
   int cmd;                               // persistent worker: the current mailbox command
   unsigned stamps[kStampPhases][kStamps];  // profiling: low 32 bits of the wall clock
 };
@@ -46,13 +47,14 @@ struct Ctx {
   bool dead;             // a poll timed out; stop waiting
   const float* input;    // event read by the INPUT phase
   bool tagged_input;     // the event is the tagged vector t_in (persistent worker)
+  bool split_wide;       // a stream wave polls the odd 1024-piece chunks of wide vectors
 #if STAMD_POLL_STAMPS
   int pph = -1;  // phase whose staging stamps the polls record (control wave)
 #endif
 
   __device__ __forceinline__ Ctx(const StepArgs& args, LdsAll& l, int grid_index, int grid_size)
       : a(args), lds(l), g(grid_index), grid(grid_size), lane(lane_id()), wave(wave_id()), t(0), valid(0),
-        slot(0), base(0), dead(false), input(args.input), tagged_input(false) {
+        slot(0), base(0), dead(false), input(args.input), tagged_input(false), split_wide(false) {
     wr = make_rsrc(a.weights, a.weight_bytes);
     kr = make_rsrc(a.keys, a.cache_bytes);
     vr = make_rsrc(a.values, a.cache_bytes);
@@ -194,15 +196,35 @@ __device__ __forceinline__ void poll_pieces(Ctx<P>& c, uint32_t tv, int n, int p
   }
 }
 
-// Whole vector of n elements padded to n_p (a multiple of 256) into dst[0 .. n_p).
+// Chunks first, first + step, ... of 1024 pieces of a wide vector into dst.
 template <int P>
-__device__ __forceinline__ void poll_vector(Ctx<P>& c, uint32_t tv, int n, int n_p, unsigned ep, float* dst) {
+__device__ __forceinline__ void poll_chunks(Ctx<P>& c, uint32_t tv, int n, int pieces, int first, int step, unsigned ep,
+                                            float* dst) {
+  for (int p0 = first * 1024; p0 < pieces; p0 += step * 1024)
+    poll_pieces<P, 16>(c, tv, n, p0, pieces - p0 < 1024 ? pieces - p0 : 1024, ep, dst + 2 * p0);
+}
+
+// Whole vector of n elements padded to n_p (a multiple of 256) into dst[0 .. n_p). With
+// `split`, a vector of more than 512 pieces is shared with the helper stream wave (see
+// help_stage): this wave polls the even 1024-piece chunks and waits for the odd ones.
+template <int P>
+__device__ __forceinline__ void poll_vector(Ctx<P>& c, uint32_t tv, int n, int n_p, unsigned ep, float* dst,
+                                            bool split = false) {
   const int pieces = n_p / 2;
   if (pieces <= 512) {
     poll_pieces<P, 8>(c, tv, n, 0, pieces, ep, dst);
+  } else if (!split) {
+    poll_chunks(c, tv, n, pieces, 0, 1, ep, dst);
   } else {
-    for (int p0 = 0; p0 < pieces; p0 += 1024)
-      poll_pieces<P, 16>(c, tv, n, p0, pieces - p0 < 1024 ? pieces - p0 : 1024, ep, dst + 2 * p0);
+    poll_chunks(c, tv, n, pieces, 0, 2, ep, dst);
+    const unsigned long long start = wall_clock64();
+    while (__hip_atomic_load(&c.lds.helped, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != ep && !c.dead) {
+      if (c.expired(start)) {
+        c.timeout();
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
   }
 }
 
@@ -390,7 +412,7 @@ __device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p, int buf, bool r
     stage_vector(c, vec[0], n, n_p / 2, ep, dst[0], raw, norm, nw);
   } else {
     // Wider vectors and the attention q/k/v carry no norm or raw copy.
-    for (int v = 0; v < nvec; v++) poll_vector(c, vec[v], n, n_p, ep, dst[v]);
+    for (int v = 0; v < nvec; v++) poll_vector(c, vec[v], n, n_p, ep, dst[v], c.split_wide && p.kind == kDown);
   }
 #if STAMD_POLL_STAMPS
   if (c.pph >= 0 && c.lane == 0) lstamp(c, c.pph, 11);
@@ -1051,6 +1073,21 @@ __global__ __launch_bounds__(kThreads) void phase_kernel(const StepArgs* __restr
   if (c.wave != 0) compute<P, A>(c, p, 0, ring);
 }
 
+// The helper stream wave (the last wave) stages the odd 1024-piece chunks of the DOWN
+// phase's activation vector while the control wave polls the even ones, so that a wide
+// vector costs one polling round trip instead of one per chunk. Mirrors the DOWN case of
+// stage_inputs (same workgroups, epoch and LDS buffer); signals through lds.helped.
+template <int P>
+__device__ __forceinline__ void help_stage(Ctx<P>& c, Phase p, int buf) {
+  const StepArgs& a = c.a;
+  if (p.kind != kDown || a.ffn_p / 2 <= 512) return;
+  if (own_units<P>(matvec_of<P>(a, p), c.grid, c.g).count == 0) return;
+  const unsigned ep = c.epoch(ph_index(kGateUp, p.layer));
+  poll_chunks(c, a.t_act, a.ffn, a.ffn_p / 2, 1, 2, ep, c.lds.xs[buf]);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the chunk's LDS writes are done
+  if (c.lane == 0) __hip_atomic_store(&c.lds.helped, ep, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 // Control wave of one forward: stage each phase's inputs once this workgroup's stream
 // waves are done with the previous phase. One barrier per phase, matching stream_loop.
 template <int P, int A>
@@ -1113,6 +1150,7 @@ __device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
 #if !STAMD_NOPF
     prefetch(c, phase_of(a, ph + 1), ring);
 #endif
+    if (c.wave == kWaves - 1) help_stage(c, phase_of(a, ph + 1), (ph + 1) & 1);
     if (stamps) lstamp(c, ph, 7);
   }
 }
@@ -1126,11 +1164,13 @@ __device__ __forceinline__ void forward(Ctx<P>& c) {
     c.lds.done[0] = 0;
     c.lds.done[1] = 0;
     c.lds.issued = 0;
+    c.lds.helped = ~0u;
   }
   for (int i = threadIdx.x; i < a.dim / 2; i += kThreads) c.lds.rope[i] = a.rope_freq[i];
   const int nst = (nph < kStampPhases ? nph : kStampPhases) * kStamps;
   if (a.stamps)
     for (int i = threadIdx.x; i < nst; i += kThreads) (&c.lds.stamps[0][0])[i] = 0u;
+  c.split_wide = true;
   if (c.wave == 0) control_loop<P, A>(c, nph);
   else stream_loop<P, A>(c, nph);
   if (a.stamps) {
