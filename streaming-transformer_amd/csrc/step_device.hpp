@@ -36,6 +36,9 @@ constexpr int kStreamWaves = kWaves - 1;
 #ifndef STAMD_PF
 #define STAMD_PF 8
 #endif
+#ifndef STAMD_OUT_EARLY
+#define STAMD_OUT_EARLY 0
+#endif
 #ifndef STAMD_PACE
 #define STAMD_PACE 0
 #endif
@@ -266,6 +269,12 @@ __device__ __forceinline__ lds_float* to_lds(float* p) { return (lds_float*)p; }
 // Store two (four) consecutive floats to LDS at p (8- or 16-byte aligned).
 __device__ __forceinline__ void lds_store2(float* p, float2 v) { *(lds_v2f*)p = v2f{v.x, v.y}; }
 __device__ __forceinline__ void lds_store4(float* p, float4 v) { *(lds_v4f*)p = v4f{v.x, v.y, v.z, v.w}; }
+// Load 16 bytes from LDS at p (16-byte aligned) as four words.
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 lds_load_u4(const float* p) {
+  const v4u v = *(const __attribute__((address_space(3))) v4u*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }

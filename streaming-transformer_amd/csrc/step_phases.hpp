@@ -48,13 +48,14 @@ struct Ctx {
   const float* input;    // event read by the INPUT phase
   bool tagged_input;     // the event is the tagged vector t_in (persistent worker)
   bool split_wide;       // a stream wave polls the odd 1024-piece chunks of wide vectors
+  bool kv_lds;           // K/V of each stream wave's first attention item are in its LDS stage
 #if STAMD_POLL_STAMPS
   int pph = -1;  // phase whose staging stamps the polls record (control wave)
 #endif
 
   __device__ __forceinline__ Ctx(const StepArgs& args, LdsAll& l, int grid_index, int grid_size)
       : a(args), lds(l), g(grid_index), grid(grid_size), lane(lane_id()), wave(wave_id()), t(0), valid(0),
-        slot(0), base(0), dead(false), input(args.input), tagged_input(false), split_wide(false) {
+        slot(0), base(0), dead(false), input(args.input), tagged_input(false), split_wide(false), kv_lds(false) {
     wr = make_rsrc(a.weights, a.weight_bytes);
     kr = make_rsrc(a.keys, a.cache_bytes);
     vr = make_rsrc(a.values, a.cache_bytes);
@@ -796,13 +797,15 @@ __device__ __forceinline__ void kv_decode(uint4 u, float* v) {
 // columns (l*E)%dim .. +E-1; the dim/E lanes of a row reduce q.k with a butterfly and the
 // output columns reduce across rows the same way. Each wave polls the q, k, v elements of
 // its own head, so attention waits only on the QKV units of that head.
-template <int P>
+// G: lanes per row (dim / E) when known at compile time, else 0. A one-wave item is a chain
+// of dependent instructions, so the reductions are specialized on G.
+template <int P, int G>
 __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ring)[kPF]) {
   const StepArgs& a = c.a;
   AttnWork w = attn_work<P>(a, c.grid, c.g, c.wave - 1);
   constexpr int E = 16 / Traits<P>::kKvBytes;
-  const int dim = a.dim, chunk = a.chunk;
-  const int group = dim / E;
+  const int dim = G ? G * E : a.dim, chunk = a.chunk;
+  const int group = G ? G : dim / E;
   const int rows_per_load = 64 / group;
   const int loads = (w.kchunks + 63) / 64;
   const int col0 = (c.lane * E) % dim;
@@ -814,9 +817,25 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
     int it = w.wid + w.nw * m;
     int h = it / w.nch, ch = it - h * w.nch;
     if (ch >= nactive) continue;
-    if (m > 0) {
-      load_block<P>(c, c.kr, p.layer, h, ch, w.kchunks, ring);
-      load_block<P>(c, c.vr, p.layer, h, ch, w.kchunks, ring + kKB);
+    // The K and V blocks: the first item's from the LDS stage (loaded by the control wave
+    // during the QKV phase) or from the ring (prefetched); later items' from memory.
+    uint4 kb[kKB], vb[kKB];
+    if (m == 0 && c.kv_lds) {
+      const float* st = c.lds.stage[c.wave - 1];
+#pragma unroll
+      for (int j = 0; j < kKB; j++) {
+        kb[j] = lds_load_u4(st + 4 * (c.lane + 64 * j));
+        vb[j] = lds_load_u4(st + 256 * kKB + 4 * (c.lane + 64 * j));
+      }
+    } else if (m == 0) {
+#pragma unroll
+      for (int j = 0; j < kKB; j++) {
+        kb[j] = ring[j];
+        vb[j] = ring[kKB + j];
+      }
+    } else {
+      load_block<P>(c, c.kr, p.layer, h, ch, w.kchunks, kb);
+      load_block<P>(c, c.vr, p.layer, h, ch, w.kchunks, vb);
     }
     // q, k, v of this lane's columns of head h (E each), polled from the tagged vectors.
     float q[E], kc[E], vc[E];
@@ -869,7 +888,7 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
       bool live = j < loads && (c.lane + 64 * j) < w.kchunks && row < chunk && row0 + row < c.valid;
       bool cur = row0 + row == c.slot;
       float k[E];
-      kv_decode<P>(ring[j], k);
+      kv_decode<P>(kb[j], k);
       float dot = 0.f;
 #pragma unroll
       for (int e = 0; e < E; e++) dot += q[e] * (cur ? kc[e] : k[e]);
@@ -889,7 +908,7 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
       int row = row_lane + j * rows_per_load;
       bool cur = row0 + row == c.slot;
       float v[E];
-      kv_decode<P>(ring[kKB + j], v);
+      kv_decode<P>(vb[j], v);
 #pragma unroll
       for (int e = 0; e < E; e++) out[e] += pr * (cur ? vc[e] : v[e]);
     }
@@ -1032,7 +1051,12 @@ __device__ __forceinline__ void compute_final(Ctx<P>& c, const float* xs_buf) {
 template <int P, int A>
 __device__ __forceinline__ void compute(Ctx<P>& c, Phase p, int buf, uint4 (&ring)[kPF]) {
   if (p.kind == kAttn) {
-    if constexpr (A == 1) compute_attn_regs(c, p, ring);
+    if constexpr (A == 1) {
+      constexpr int E = 16 / Traits<P>::kKvBytes;
+      if (c.a.dim == 16 * E) compute_attn_regs<P, 16>(c, p, ring);
+      else if (c.a.dim == 8 * E) compute_attn_regs<P, 8>(c, p, ring);
+      else compute_attn_regs<P, 0>(c, p, ring);
+    }
     else compute_attn_lds(c, p, ring);
   } else if (p.kind != kFinal) {
     compute_matvec(c, p, c.lds.xs[buf], c.lds.xres[p.kind == kDown ? 1 : 0], ring);
@@ -1073,6 +1097,32 @@ __global__ __launch_bounds__(kThreads) void phase_kernel(const StepArgs* __restr
   if (c.wave != 0) compute<P, A>(c, p, 0, ring);
 }
 
+// Control wave, at the start of a layer's QKV phase: load the K and V blocks of each stream
+// wave's first attention item of the layer into that wave's LDS stage, with loads that write
+// LDS directly (K at stage[0 ..), V at stage[256 * kKB ..), 16-byte chunk i at float 4i).
+// The blocks do not depend on this step's q, k, v (attention takes the current slot's row from
+// k and v), so they stream while the QKV phase runs, and the stream waves' rings can
+// prefetch the OUT weights instead.
+template <int P>
+__device__ __forceinline__ void load_kv_to_lds(Ctx<P>& c, int layer) {
+  typedef __attribute__((address_space(3))) void lds_void;
+  const StepArgs& a = c.a;
+  const int nactive = (c.valid + a.chunk - 1) / a.chunk;
+  for (int sw = 0; sw < kStreamWaves; sw++) {
+    const AttnWork w = attn_work<P>(a, c.grid, c.g, sw);
+    if (w.items == 0) break;  // items go to waves in order: none for later waves either
+    const int h = w.wid / w.nch, ch = w.wid - h * w.nch;
+    if (ch >= nactive) continue;
+    float* st = c.lds.stage[sw];
+#pragma unroll
+    for (int j = 0; j < kKB; j++) {
+      const uint32_t off = attn_chunk_offset<P>(a, layer, h, ch, c.lane + 64 * j, w.kchunks);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(c.kr, (lds_void*)to_lds(st + 256 * j), 16, (int)off, 0, 0, 1);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(c.vr, (lds_void*)to_lds(st + 256 * (kKB + j)), 16, (int)off, 0, 0, 1);
+    }
+  }
+}
+
 // The helper stream wave (the last wave) stages the odd 1024-piece chunks of the DOWN
 // phase's activation vector while the control wave polls the even ones, so that a wide
 // vector costs one polling round trip instead of one per chunk. Mirrors the DOWN case of
@@ -1105,6 +1155,8 @@ __device__ __forceinline__ void control_loop(Ctx<P>& c, int nph) {
       if (stamps && c.g == 0) put_global(a.stamps, (size_t)kStamps * c.grid * nph, wall_clock64());
       break;
     }
+    if constexpr (A == 1)
+      if (c.kv_lds && p.kind == kQkv) load_kv_to_lds(c, p.layer);
     // Start polling for the next phase's inputs only once this workgroup's own part of
     // the current phase is done: the producers elsewhere finish at about the same time,
     // and polling earlier would only add memory traffic.
@@ -1116,6 +1168,8 @@ __device__ __forceinline__ void control_loop(Ctx<P>& c, int nph) {
     c.pph = a.stamps ? ph : -1;
 #endif
     stage_inputs<P, A>(c, phase_of(a, ph + 1), (ph + 1) & 1, true);
+    // The attention phase reads the K/V blocks loaded above once the barrier is passed.
+    if (A == 1 && c.kv_lds && p.kind == kQkv) __builtin_amdgcn_s_waitcnt(0);
     if (stamps) lstamp(c, ph, 3);
   }
 }
@@ -1148,7 +1202,18 @@ __device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
       __builtin_amdgcn_s_sleep(1);
 #endif
 #if !STAMD_NOPF
-    prefetch(c, phase_of(a, ph + 1), ring);
+    {
+      // With the attention K/V in LDS the ring has nothing to prefetch for attention. It
+      // stays empty, so that the attention phase's stores and polls find this CU's memory
+      // queue empty; OUT is prefetched after attention.
+      const Phase nxt = phase_of(a, ph + 1);
+#if STAMD_OUT_EARLY
+      if (A == 1 && c.kv_lds && nxt.kind == kAttn) prefetch(c, phase_of(a, ph + 2), ring);
+      else if (!(A == 1 && c.kv_lds && p.kind == kAttn)) prefetch(c, nxt, ring);
+#else
+      if (!(A == 1 && c.kv_lds && nxt.kind == kAttn)) prefetch(c, nxt, ring);
+#endif
+    }
 #endif
     if (c.wave == kWaves - 1) help_stage(c, phase_of(a, ph + 1), (ph + 1) & 1);
     if (stamps) lstamp(c, ph, 7);
@@ -1171,6 +1236,7 @@ __device__ __forceinline__ void forward(Ctx<P>& c) {
   if (a.stamps)
     for (int i = threadIdx.x; i < nst; i += kThreads) (&c.lds.stamps[0][0])[i] = 0u;
   c.split_wide = true;
+  c.kv_lds = A == 1;
   if (c.wave == 0) control_loop<P, A>(c, nph);
   else stream_loop<P, A>(c, nph);
   if (a.stamps) {
