@@ -20,14 +20,24 @@
 
 namespace stamd {
 
+// A stream wave's share of one matvec kind. The share depends on the kind, the grid and the
+// wave, not on the layer (which only moves the weight base), so a forward computes it once.
+struct WaveSplit {
+  int slabs, per_unit, slabs_row, unit0, unit;
+  uint32_t base_rel, unit_stride;  // first owned unit from the matrix start; stride between units
+  uint32_t refill_off, last_off;   // unit offsets (from the matrix start) of slab kPF and the last slab
+  int refill_r, last_r;            // slab within that unit
+};
+
 struct LdsAll {
   float xs[2][kXs];                      // phase input vector, double buffered by phase parity
   float xres[2][kMaxDim];                // x before this layer (OUT residual) and after OUT (DOWN residual)
   float qkv[3 * kMaxDim];                // attention LDS path: q, k, v of the step
   float stage[kStreamWaves][kAttnLds];   // attention LDS path: per-wave K/V staging
   float probs[kStreamWaves][64];
-  float sums[kStreamWaves][kPF][2];      // row sums of units finished in the current ring pass
-  float rope[kMaxDim / 2];               // RoPE inverse frequencies
+  float rope_cos[kMaxDim / 2];           // RoPE cos / sin of this step's position per pair
+  float rope_sin[kMaxDim / 2];
+  WaveSplit split[kStreamWaves][kFinal];  // per stream wave and matvec kind (forward only)
   unsigned done[2];                      // stream waves finished with the phase of this parity
   unsigned issued;                       // stream-wave phases whose results are issued, this forward
   unsigned helped;                       // epoch of the wide vector whose odd chunks the helper staged
@@ -49,13 +59,14 @@ struct Ctx {
   bool tagged_input;     // the event is the tagged vector t_in (persistent worker)
   bool split_wide;       // a stream wave polls the odd 1024-piece chunks of wide vectors
   bool kv_lds;           // K/V of each stream wave's first attention item are in its LDS stage
+  bool split_ready;      // lds.split holds this wave's matvec shares
 #if STAMD_POLL_STAMPS
   int pph = -1;  // phase whose staging stamps the polls record (control wave)
 #endif
 
   __device__ __forceinline__ Ctx(const StepArgs& args, LdsAll& l, int grid_index, int grid_size)
       : a(args), lds(l), g(grid_index), grid(grid_size), lane(lane_id()), wave(wave_id()), t(0), valid(0),
-        slot(0), base(0), dead(false), input(args.input), tagged_input(false), split_wide(false), kv_lds(false) {
+        slot(0), base(0), dead(false), input(args.input), tagged_input(false), split_wide(false), kv_lds(false), split_ready(false) {
     wr = make_rsrc(a.weights, a.weight_bytes);
     kr = make_rsrc(a.keys, a.cache_bytes);
     vr = make_rsrc(a.values, a.cache_bytes);
@@ -178,6 +189,19 @@ __device__ __forceinline__ void poll_regs(Ctx<P>& c, uint32_t tv, int n, int p0,
 #if STAMD_POLL_STAMPS
   if (c.pph >= 0 && c.lane == 0) lstamp(c, c.pph, 10);
 #endif
+}
+
+// True when every piece this lane holds (pieces below np) carries epoch ep.
+template <int NP>
+__device__ __forceinline__ bool pieces_current(const uint4 (&buf)[NP], int lane, int n, int p0, int np, unsigned ep) {
+  bool ok = true;
+#pragma unroll
+  for (int k = 0; k < NP; k++) {
+    int pc = lane + 64 * k;
+    int e0 = 2 * (p0 + pc);
+    ok = ok && (pc >= np || ((e0 >= n || buf[k].y == ep) && (e0 + 1 >= n || buf[k].w == ep)));
+  }
+  return ok;
 }
 
 // Value pair of piece k (0 for padding at or beyond n).
@@ -439,11 +463,50 @@ __device__ __forceinline__ WaveWork work_of(const Mv& m, int grid, int g, int sw
   return w;
 }
 
+// A stream wave's share of matvec phase p: from the forward's table when it is filled, else
+// computed. unit0 is the first owned unit; refill and last are the cursors of slab kPF and of
+// the last slab.
 template <int P>
-__device__ __forceinline__ void prefetch_matvec(Ctx<P>& c, const WaveWork& w, uint4 (&ring)[kPF]) {
+__device__ __forceinline__ WaveWork wave_work(Ctx<P>& c, Phase p, int sw, int& unit0, int& unit, SlabCursor& refill,
+                                              SlabCursor& last) {
+  const Mv m = matvec_of<P>(c.a, p);
+  if (c.split_ready) {
+    const WaveSplit sp = c.lds.split[sw][p.kind];
+    unit0 = sp.unit0;
+    unit = sp.unit;
+    refill = {m.woff + sp.refill_off, sp.refill_r};
+    last = {m.woff + sp.last_off, sp.last_r};
+    return {sp.slabs_row, sp.per_unit, sp.slabs, m.woff + sp.base_rel, sp.unit_stride};
+  }
+  WaveWork w = work_of<P>(m, c.grid, c.g, sw, unit0);
+  unit = m.unit;
+  refill = cursor_at(w, kPF);
+  last = cursor_at(w, w.slabs > 0 ? w.slabs - 1 : 0);
+  return w;
+}
+
+// Fill lds.split for this stream wave (once per forward; read back only by this wave).
+template <int P>
+__device__ __forceinline__ void fill_split(Ctx<P>& c) {
+  const int sw = c.wave - 1;
+  for (int kind = kInput; kind < kFinal; kind++) {
+    if (kind == kAttn) continue;
+    Mv m = matvec_of<P>(c.a, Phase{kind, 0});
+    m.woff = 0;
+    int unit0;
+    const WaveWork w = work_of<P>(m, c.grid, c.g, sw, unit0);
+    const SlabCursor r = cursor_at(w, kPF), l = cursor_at(w, w.slabs > 0 ? w.slabs - 1 : 0);
+    if (c.lane == 0)
+      c.lds.split[sw][kind] = WaveSplit{w.slabs, w.per_unit, w.slabs_row, unit0, m.unit, w.base, w.unit_stride,
+                                        r.unit_off, l.unit_off, r.r, l.r};
+  }
+  c.split_ready = true;
+}
+
+template <int P>
+__device__ __forceinline__ void prefetch_matvec(Ctx<P>& c, const WaveWork& w, SlabCursor last, uint4 (&ring)[kPF]) {
   if (w.slabs == 0) return;
-  SlabCursor cur = cursor_at(w, 0);
-  SlabCursor last = cursor_at(w, w.slabs - 1);
+  SlabCursor cur{w.base, 0};
 #pragma unroll
   for (int j = 0; j < kPF; j++) {
     ring[j] = ld16(c.wr, (j < w.slabs ? cur : last).offset(c.lane));
@@ -497,10 +560,10 @@ __device__ __forceinline__ void prefetch(Ctx<P>& c, Phase p, uint4 (&ring)[kPF])
     load_block<P>(c, c.kr, p.layer, h, ch, w.kchunks, ring);
     load_block<P>(c, c.vr, p.layer, h, ch, w.kchunks, ring + kKB);
   } else if (p.kind != kFinal) {
-    Mv m = matvec_of<P>(c.a, p);
-    int unit0;
-    WaveWork w = work_of<P>(m, c.grid, c.g, sw, unit0);
-    prefetch_matvec(c, w, ring);
+    int unit0, unit;
+    SlabCursor refill, last;
+    const WaveWork w = wave_work(c, p, sw, unit0, unit, refill, last);
+    prefetch_matvec(c, w, last, ring);
   }
 }
 
@@ -515,14 +578,13 @@ __device__ __forceinline__ void epilogue(Ctx<P>& c, Phase p, int unit, float s0,
       break;
     case kQkv: {
       int r0 = unit * 2;
-      int sec = r0 / a.width;
+      int sec = (r0 >= a.width) + (r0 >= 2 * a.width);
       int i = r0 - sec * a.width;
       float va = cast<P>(s0), vb = cast<P>(s1);
       if (sec < 2) {
         // RoPE on the adjacent pair (i, i+1), src/cuda/Primitives.cuh:148-159
-        int e = i % a.dim;
-        float angle = (float)c.t * c.lds.rope[e >> 1];
-        float co = cosf(angle), si = sinf(angle);
+        int e = (a.dim & (a.dim - 1)) == 0 ? (i & (a.dim - 1)) : i % a.dim;
+        float co = c.lds.rope_cos[e >> 1], si = c.lds.rope_sin[e >> 1];
         float ra = cast<P>(va * co - vb * si);
         float rb = cast<P>(va * si + vb * co);
         uint32_t tv = sec == 0 ? a.t_q : a.t_k;
@@ -556,14 +618,13 @@ __device__ __forceinline__ void epilogue(Ctx<P>& c, Phase p, int unit, float s0,
 template <int P>
 __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* xs_buf, const float* xres,
                                                uint4 (&ring)[kPF]) {
-  Mv m = matvec_of<P>(c.a, p);
-  int unit;
-  WaveWork w = work_of<P>(m, c.grid, c.g, c.wave - 1, unit);
+  int unit, munit;
+  SlabCursor refill, last;
+  const WaveWork w = wave_work(c, p, c.wave - 1, unit, munit, refill, last);
   if (w.slabs == 0) return;
-  float (*sums)[2] = c.lds.sums[c.wave - 1];
-  SlabCursor refill = cursor_at(w, kPF);
   int ru = 0, s = 0;  // row within the unit, slab within the row
   float acc0 = 0.f, acc1 = 0.f;
+  float su0 = 0.f, su1 = 0.f;  // lane k: row sums of the k-th unit finished in this ring pass
   const float* xs = xs_buf + c.lane * Traits<P>::kEpc;
   if (c.wave == 1) stamp(c, p, 4);
   for (int base = 0; base < w.slabs; base += kPF) {
@@ -583,13 +644,13 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* 
         }
         if (++s == w.slabs_row) {
           s = 0;
-          if (++ru == m.unit) {
+          if (++ru == munit) {
             ru = 0;
             float s0 = wave_total(acc0);
-            float s1 = m.unit == 2 ? wave_total(acc1) : 0.f;
-            if (c.lane == 0) {
-              sums[finished][0] = s0;
-              sums[finished][1] = s1;
+            float s1 = munit == 2 ? wave_total(acc1) : 0.f;
+            if (c.lane == finished) {
+              su0 = s0;
+              su1 = s1;
             }
             finished++;
             acc0 = 0.f;
@@ -598,9 +659,8 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* 
         }
       }
     }
-    // Epilogues of the finished units, outside the unrolled loop (one copy of the code).
-    if (c.lane == 0)
-      for (int k = 0; k < finished; k++) epilogue(c, p, unit + kStreamWaves * k, sums[k][0], sums[k][1], xres);
+    // Epilogues of the finished units, one unit per lane, outside the unrolled loop.
+    if (c.lane < finished) epilogue(c, p, unit + kStreamWaves * c.lane, su0, su1, xres);
     unit += kStreamWaves * finished;
   }
   if (c.wave == 1) stamp(c, p, 6);
@@ -1071,6 +1131,17 @@ __device__ __forceinline__ void lds_barrier() {
 // ---------------------------------------------------------------------------------------------
 // kernels
 
+// RoPE cos / sin of this step's position for each pair of a head (src/cuda/Primitives.cuh:
+// 148-159): angle = position * inverse frequency, computed once per step instead of per unit.
+template <int P>
+__device__ __forceinline__ void fill_rope(Ctx<P>& c) {
+  for (int i = threadIdx.x; i < c.a.dim / 2; i += kThreads) {
+    const float angle = (float)c.t * c.a.rope_freq[i];
+    c.lds.rope_cos[i] = cosf(angle);
+    c.lds.rope_sin[i] = sinf(angle);
+  }
+}
+
 // One phase per launch (staged and graph backends). The FINAL launch advances the epoch.
 template <int P, int A>
 __global__ __launch_bounds__(kThreads) void phase_kernel(const StepArgs* __restrict__ ap, int ph) {
@@ -1082,7 +1153,7 @@ __global__ __launch_bounds__(kThreads) void phase_kernel(const StepArgs* __restr
   c.base = load_epoch(a);
   c.set_position(load_position(a));
   uint4 ring[kPF];
-  for (int i = threadIdx.x; i < a.dim / 2; i += kThreads) c.lds.rope[i] = a.rope_freq[i];
+  fill_rope(c);
   if (c.wave == 0) stage_inputs<P, A>(c, p, 0, false);
   else prefetch(c, p, ring);
   lds_barrier();
@@ -1180,6 +1251,7 @@ template <int P, int A>
 __device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
   const StepArgs& a = c.a;
   const bool stamps = a.stamps && c.wave == 1 && c.lane == 0;
+  fill_split(c);
   uint4 ring[kPF];
 #if !STAMD_NOPF
   prefetch(c, phase_of(a, 0), ring);
@@ -1231,7 +1303,7 @@ __device__ __forceinline__ void forward(Ctx<P>& c) {
     c.lds.issued = 0;
     c.lds.helped = ~0u;
   }
-  for (int i = threadIdx.x; i < a.dim / 2; i += kThreads) c.lds.rope[i] = a.rope_freq[i];
+  fill_rope(c);
   const int nst = (nph < kStampPhases ? nph : kStampPhases) * kStamps;
   if (a.stamps)
     for (int i = threadIdx.x; i < nst; i += kThreads) (&c.lds.stamps[0][0])[i] = 0u;
