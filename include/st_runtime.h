@@ -155,6 +155,28 @@ int st_runtime_info_json(st_runtime* runtime, char* buffer, size_t cap, size_t* 
 /* Json probe() - src/cuda/Runtime.cu:134-161, as a JSON string. */
 int st_probe_json(char* buffer, size_t cap, size_t* needed);
 
+/* Extension (no counterpart in the reference, which is single-stream by design,
+ * docs/Architecture.md:3): `streams` independent streams (1..256) sharing one set of
+ * weights, each with its own K/V ring, hidden state and position. FP32 checkpoints only
+ * (mixed must be 0); weight_dtype as in st_options. A step advances every stream by one
+ * event; the projections run as MFMA GEMMs over the streams. */
+typedef struct st_batch st_batch;
+int st_batch_create(const st_config* config, int32_t mixed, const st_tensor* tensors, size_t tensor_count,
+                    int32_t streams, int32_t weight_dtype, st_batch** out);
+void st_batch_destroy(st_batch* batch);
+/* inputs: streams*features floats (stream-major); scores: streams floats. */
+int st_batch_step(st_batch* batch, const float* inputs, float* scores);
+/* Zero stream `stream` (all streams when -1): K/V, hidden state and position. */
+int st_batch_reset(st_batch* batch, int32_t stream);
+/* State of one stream, in st_runtime_snapshot's layout; any output may be NULL. */
+int st_batch_snapshot(st_batch* batch, int32_t stream, uint64_t* position, float* keys, float* values,
+                      float* hidden);
+/* `count` steps from a preloaded device copy of count*streams*features inputs, continuing
+ * the current state; a HIP event after each step. Writes the mean microseconds per step and,
+ * when per_step_us is not NULL, each step's event-to-event duration. */
+int st_batch_device_run(st_batch* batch, const float* inputs, size_t count, double* us_per_step,
+                        double* per_step_us);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* st_last_error(void);
 

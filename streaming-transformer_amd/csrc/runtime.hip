@@ -4,6 +4,7 @@
 // the K/V rings, an FP32 scratch arena, the epoch-tagged activation vectors, the
 // device-held position and epoch. Mirrors Stream::Runtime::Impl (src/cuda/Runtime.cu:167-653) behind a C ABI.
 #include "step_phases.hpp"
+#include "batch_kernels.hpp"
 #include "../../include/st_runtime.h"
 
 #include <hip/hip_runtime.h>
@@ -455,7 +456,11 @@ int Runtime::legal_blocks_t() {
 // Weight arena in phase order: input, then per layer norm1, norm2, qkv (stacked q;k;v),
 // out, gateup (row 2i = gate i, row 2i+1 = up i), down; then final_norm, score.
 // Rows are padded with zeros to a multiple of 16 bytes.
-void Runtime::build_weights(const st_tensor* tensors, size_t count) {
+// The weight arena (also used by the batched runtime): rows padded to whole 1 KiB slabs, q/k/v
+// stacked, gate and up rows interleaved per unit; offsets recorded in args_. The row lengths
+// args_.width_p, ffn_p and features_p must be set.
+static void build_arena(const st_config& c_, int prec_, const st_tensor* tensors, size_t count, StepArgs& args_,
+                        DeviceBuffer& weights_) {
   std::map<std::string, const st_tensor*> byname;
   for (size_t i = 0; i < count; i++) {
     if (!tensors[i].name || !tensors[i].data) throw Error(ST_ERR_INVALID, "Null tensor");
@@ -549,6 +554,10 @@ void Runtime::build_weights(const st_tensor* tensors, size_t count) {
   HIP_CHECK(hipMemcpy(weights_.ptr, host.data(), host.size(), hipMemcpyHostToDevice));
   a.weights = reinterpret_cast<const char*>(weights_.ptr);
   a.weight_bytes = (uint32_t)host.size();
+}
+
+void Runtime::build_weights(const st_tensor* tensors, size_t count) {
+  build_arena(c_, prec_, tensors, count, args_, weights_);
 }
 
 template <int P, int A>
@@ -893,6 +902,8 @@ std::string Runtime::info() {
   return o.str();
 }
 
+#include "batch_runtime.hpp"
+
 }  // namespace stamd
 
 // ---------------------------------------------------------------------------------------------
@@ -1024,6 +1035,61 @@ int st_runtime_info_json(st_runtime* r, char* buffer, size_t cap, size_t* needed
 
 int st_probe_json(char* buffer, size_t cap, size_t* needed) {
   return guarded([&] { write_string(stamd::probe_json(), buffer, cap, needed); });
+}
+
+// ---- batched independent streams (extension)
+
+struct st_batch {
+  std::unique_ptr<stamd::Batch> impl;
+};
+
+int st_batch_create(const st_config* config, int32_t mixed, const st_tensor* tensors, size_t count, int32_t streams,
+                    int32_t weight_dtype, st_batch** out) {
+  return guarded([&] {
+    if (!config || !tensors || !out) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    *out = nullptr;
+    if (mixed) throw stamd::Error(ST_ERR_INVALID, "Batched streams take FP32 checkpoints (FP32 or bfloat16 weights)");
+    auto r = std::make_unique<st_batch>();
+    r->impl = std::make_unique<stamd::Batch>(*config, tensors, count, streams, weight_dtype);
+    *out = r.release();
+  });
+}
+
+void st_batch_destroy(st_batch* r) {
+  if (!r) return;
+  try {
+    r->impl.reset();
+  } catch (...) {
+  }
+  delete r;
+}
+
+int st_batch_step(st_batch* r, const float* inputs, float* scores) {
+  return guarded([&] {
+    if (!r) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    r->impl->step(inputs, scores);
+  });
+}
+
+int st_batch_reset(st_batch* r, int32_t stream) {
+  return guarded([&] {
+    if (!r) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    r->impl->reset(stream);
+  });
+}
+
+int st_batch_snapshot(st_batch* r, int32_t stream, uint64_t* position, float* keys, float* values, float* hidden) {
+  return guarded([&] {
+    if (!r) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    r->impl->snapshot(stream, position, keys, values, hidden);
+  });
+}
+
+int st_batch_device_run(st_batch* r, const float* inputs, size_t count, double* us_per_step, double* per_step_us) {
+  return guarded([&] {
+    if (!r || !us_per_step) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    *us_per_step = r->impl->device_run(inputs, count, per_step_us);
+  });
 }
 
 const char* st_last_error(void) { return stamd::g_last_error.c_str(); }

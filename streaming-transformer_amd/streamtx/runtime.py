@@ -103,7 +103,16 @@ def library(path: os.PathLike | None = None) -> ctypes.CDLL:
     lib.st_probe_json.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_last_error.argtypes = []
     lib.st_last_error.restype = ctypes.c_char_p
-    for name in ('st_runtime_create', 'st_runtime_step', 'st_runtime_reset', 'st_runtime_stop',
+    lib.st_batch_create.argtypes = [ctypes.POINTER(_Config), ctypes.c_int32, ctypes.POINTER(_Tensor),
+                                    ctypes.c_size_t, ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(P)]
+    lib.st_batch_destroy.argtypes = [P]
+    lib.st_batch_destroy.restype = None
+    lib.st_batch_step.argtypes = [P, F, F]
+    lib.st_batch_reset.argtypes = [P, ctypes.c_int32]
+    lib.st_batch_snapshot.argtypes = [P, ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64), F, F, F]
+    lib.st_batch_device_run.argtypes = [P, F, ctypes.c_size_t, D, D]
+    for name in ('st_batch_create', 'st_batch_step', 'st_batch_reset', 'st_batch_snapshot', 'st_batch_device_run',
+                 'st_runtime_create', 'st_runtime_step', 'st_runtime_reset', 'st_runtime_stop',
                  'st_runtime_snapshot', 'st_runtime_device_trace', 'st_runtime_device_run', 'st_runtime_phase_times',
                  'st_runtime_info_json',
                  'st_probe_json'):
@@ -129,6 +138,25 @@ def _json(fn, *args) -> dict:
     return json.loads(buf.value.decode())
 
 
+def _marshal(config, tensors):
+    """(st_config, kept arrays, st_tensor array) for a create call. Every named tensor is
+    passed; the library validates names, shapes and the config."""
+    cfg = _Config(config.layers, config.width, config.heads, config.ffn, config.window,
+                  config.features, config.epsilon)
+    keep, items = [], []
+    for name in sorted(tensors):
+        a = np.ascontiguousarray(tensors[name], dtype=np.float32)
+        keep.append(a)
+        t = _Tensor()
+        t.name = name.encode()
+        t.rank = a.ndim
+        t.shape[0] = a.shape[0]
+        t.shape[1] = a.shape[1] if a.ndim > 1 else 0
+        t.data = _fptr(a)
+        items.append(t)
+    return cfg, keep, (_Tensor * len(items))(*items)
+
+
 def probe() -> dict:
     """Stream::probe() (src/cuda/Runtime.cu:134-161)."""
     return _json(library().st_probe_json)
@@ -147,27 +175,13 @@ class Runtime:
         self.mixed = bool(mixed)
         self.options = options or RuntimeOptions()
         lib = library()
-        cfg = _Config(config.layers, config.width, config.heads, config.ffn, config.window,
-                      config.features, config.epsilon)
-        keep, items = [], []
-        # Pass every named tensor; the library validates names, shapes and the config.
-        for name in sorted(tensors):
-            a = np.ascontiguousarray(tensors[name], dtype=np.float32)
-            keep.append(a)
-            t = _Tensor()
-            t.name = name.encode()
-            t.rank = a.ndim
-            t.shape[0] = a.shape[0]
-            t.shape[1] = a.shape[1] if a.ndim > 1 else 0
-            t.data = _fptr(a)
-            items.append(t)
-        array = (_Tensor * len(items))(*items)
+        cfg, keep, array = _marshal(config, tensors)
         o = self.options
         opts = _Options(int(o.backend), int(o.blocks), int(o.backoff), int(o.mapped), int(o.vector_matvec),
                         int(o.fused_attention), int(o.max_events), int(o.initial_sequence),
                         float(o.idle_seconds), int(o.weight_dtype), 0)
         handle = ctypes.c_void_p()
-        _check(lib.st_runtime_create(ctypes.byref(cfg), int(self.mixed), array, len(items), ctypes.byref(opts),
+        _check(lib.st_runtime_create(ctypes.byref(cfg), int(self.mixed), array, len(array), ctypes.byref(opts),
                                      ctypes.byref(handle)))
         self._h = handle
         self._score = np.zeros(1, dtype=np.float32)
@@ -258,3 +272,79 @@ class Runtime:
 
     def info(self) -> dict:
         return _json(library().st_runtime_info_json, self._handle())
+
+
+class BatchRuntime:
+    """`streams` independent streams over one set of weights (extension; the reference is
+    single-stream, docs/Architecture.md:3). Each stream behaves like its own Runtime on the
+    same events; a step advances all of them. FP32 checkpoints, weights stored as
+    ``weight_dtype`` (WeightStorage)."""
+
+    def __init__(self, model, streams: int, weight_dtype: int = 0):
+        if isinstance(model, Checkpoint):
+            config, tensors, mixed = model.config, model.tensors, model.mixed
+        else:
+            config, tensors, mixed = model
+        self.config: ModelConfig = config
+        self.streams = int(streams)
+        cfg, keep, array = _marshal(config, tensors)
+        handle = ctypes.c_void_p()
+        _check(library().st_batch_create(ctypes.byref(cfg), int(bool(mixed)), array, len(array), self.streams,
+                                         int(weight_dtype), ctypes.byref(handle)))
+        self._h = handle
+        self._scores = np.zeros(self.streams, dtype=np.float32)
+
+    def close(self) -> None:
+        if getattr(self, '_h', None):
+            library().st_batch_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _handle(self):
+        if not self._h:
+            raise RuntimeError('BatchRuntime is closed')
+        return self._h
+
+    def step(self, events) -> np.ndarray:
+        """events [streams, features] -> scores [streams]."""
+        x = np.ascontiguousarray(events, dtype=np.float32)
+        if x.size != self.streams * self.config.features:
+            raise ValueError('events must hold streams*features floats')
+        _check(library().st_batch_step(self._handle(), _fptr(x), _fptr(self._scores)))
+        return self._scores.copy()
+
+    def reset(self, stream: int = -1) -> None:
+        """Zero one stream (all when -1)."""
+        _check(library().st_batch_reset(self._handle(), int(stream)))
+
+    def snapshot(self, stream: int):
+        """Runtime.snapshot() of one stream."""
+        c = self.config
+        keys = np.empty((c.layers, c.heads, c.window, c.dim), dtype=np.float32)
+        values = np.empty_like(keys)
+        hidden = np.empty((c.layers, c.width), dtype=np.float32)
+        pos = ctypes.c_uint64(0)
+        _check(library().st_batch_snapshot(self._handle(), int(stream), ctypes.byref(pos), _fptr(keys),
+                                           _fptr(values), _fptr(hidden)))
+        return int(pos.value), keys, values, hidden
+
+    def device_run(self, inputs):
+        """Steps from a preloaded device copy of inputs [count, streams, features]; continues
+        the current state. (mean us per step, per-step us)."""
+        x = np.ascontiguousarray(inputs, dtype=np.float32).reshape(-1, self.streams * self.config.features)
+        per = np.empty(x.shape[0], dtype=np.float64)
+        mean = ctypes.c_double(0)
+        _check(library().st_batch_device_run(self._handle(), _fptr(x), x.shape[0], ctypes.byref(mean),
+                                             per.ctypes.data_as(ctypes.POINTER(ctypes.c_double))))
+        return float(mean.value), per

@@ -1,0 +1,164 @@
+"""Batched independent streams (st_batch_*): B streams over one set of weights, the
+projections as MFMA GEMMs over the streams.
+
+Bars, through the C ABI:
+  - every stream against its own CPU oracle (FP64-accumulating): FP32 within 1e-6 + 1e-5|r|
+    per step, for the score and the stream's complete carried state;
+  - a stream's results do not depend on the batch around it: stream b of a batch of B is
+    bit-identical to a batch of 1 fed the same events (every output element of the MFMA
+    tiles and the split-K reduction is a function of that stream's row only);
+  - per-stream reset touches only its stream; device_run equals stepping bit for bit.
+"""
+import numpy as np
+import pytest
+
+from oracle.pyoracle import Oracle
+from streamtx import BatchRuntime, ModelConfig, WeightStorage, numerical, round_bf16, synthetic_checkpoint
+
+pytestmark = pytest.mark.gpu
+
+STRICT = dict(atol=1e-6, rtol=1e-5)
+
+SHAPES = {
+    'small': ModelConfig(4, 256, 4, 1024, 64, 256),
+    'main': ModelConfig(8, 512, 8, 2048, 128, 512),
+    # head dim 32, 32 features (padded input rows), window 256
+    'ref-main': ModelConfig(2, 128, 4, 256, 256, 32),
+    # head dim 48
+    'dh48': ModelConfig(2, 96, 2, 192, 40, 96),
+}
+
+
+def batch(model, streams, weight_dtype=WeightStorage.AS_MODEL):
+    c = model[0]
+    print(f'[case] batch streams={streams} layers={c.layers} width={c.width} window={c.window} '
+          f'weights={WeightStorage(weight_dtype).name}', flush=True)
+    return BatchRuntime(model, streams, weight_dtype)
+
+
+def _events(config, seed, steps, streams):
+    return np.random.default_rng(seed).standard_normal((steps, streams, config.features)).astype(np.float32)
+
+
+def _check_state(state, oracle_state):
+    assert state[0] == oracle_state[0]
+    for a, o in zip(state[1:], oracle_state[1:]):
+        assert numerical.fp32_strict_failures(a, o, **STRICT) == 0, float(np.abs(a - o).max())
+
+
+@pytest.mark.parametrize('name,streams,steps,resets', [
+    ('small', 19, 80, {7: 50, 18: 3}),
+    ('ref-main', 17, 270, {0: 100}),
+    ('dh48', 3, 60, {1: 41}),
+    ('main', 16, 24, {5: 11}),
+])
+def test_every_stream_matches_oracle(name, streams, steps, resets):
+    c = SHAPES[name]
+    w = synthetic_checkpoint(c, seed=11)
+    events = _events(c, 11, steps, streams)
+    oracles = [Oracle(c, w, accumulate='double', threads=8) for _ in range(streams)]
+    with batch((c, w, False), streams) as rt:
+        for i in range(steps):
+            for b, at in resets.items():
+                if at == i:
+                    rt.reset(b)
+                    oracles[b].reset()
+            got = rt.step(events[i])
+            for b in range(streams):
+                ref = oracles[b].step(events[i, b])
+                assert numerical.fp32_strict_failures([got[b]], [ref], **STRICT) == 0, (i, b, got[b], ref)
+        for b in range(streams):
+            _check_state(rt.snapshot(b), oracles[b].snapshot())
+
+
+def test_bf16_weights_match_oracle_on_rounded_weights():
+    c = SHAPES['main']
+    w = synthetic_checkpoint(c, seed=12)
+    rounded = {k: round_bf16(v) for k, v in w.items()}
+    streams, steps = 16, 20
+    events = _events(c, 12, steps, streams)
+    oracles = [Oracle(c, rounded, accumulate='double', threads=8) for _ in range(streams)]
+    with batch((c, w, False), streams, WeightStorage.BF16) as rt:
+        for i in range(steps):
+            got = rt.step(events[i])
+            for b in range(streams):
+                ref = oracles[b].step(events[i, b])
+                assert numerical.fp32_strict_failures([got[b]], [ref], **STRICT) == 0, (i, b, got[b], ref)
+        for b in (0, 9, 15):
+            _check_state(rt.snapshot(b), oracles[b].snapshot())
+
+
+@pytest.mark.parametrize('weight_dtype', [WeightStorage.AS_MODEL, WeightStorage.BF16])
+def test_stream_independent_of_batch(weight_dtype):
+    c = SHAPES['small']
+    w = synthetic_checkpoint(c, seed=13)
+    steps, streams = 70, 40
+    events = _events(c, 13, steps, streams)
+    with batch((c, w, False), streams, weight_dtype) as rt:
+        many = np.stack([rt.step(events[i]) for i in range(steps)])
+        states = [rt.snapshot(b) for b in (0, 21, 39)]
+    for b, state in zip((0, 21, 39), states):
+        with batch((c, w, False), 1, weight_dtype) as one:
+            alone = np.array([one.step(events[i, b:b + 1])[0] for i in range(steps)], dtype=np.float32)
+            np.testing.assert_array_equal(alone, many[:, b])
+            ref = one.snapshot(0)
+        assert ref[0] == state[0]
+        for x, y in zip(ref[1:], state[1:]):
+            np.testing.assert_array_equal(x, y)
+
+
+def test_reset_one_and_all_and_device_run_equals_stepping():
+    c = SHAPES['small']
+    w = synthetic_checkpoint(c, seed=14)
+    streams, steps = 5, 30
+    events = _events(c, 14, steps, streams)
+    with batch((c, w, False), streams) as rt:
+        for i in range(10):
+            rt.step(events[i])
+        before = [rt.snapshot(b) for b in range(streams)]
+        rt.reset(2)
+        after = [rt.snapshot(b) for b in range(streams)]
+        assert after[2][0] == 0
+        for a in after[2][1:]:
+            assert not a.any()
+        for b in (0, 1, 3, 4):
+            assert after[b][0] == before[b][0] == 10
+            for x, y in zip(after[b][1:], before[b][1:]):
+                np.testing.assert_array_equal(x, y)
+        rt.reset()
+        assert all(rt.snapshot(b)[0] == 0 for b in range(streams))
+        stepped = np.stack([rt.step(events[i]) for i in range(steps)])
+        states = [rt.snapshot(b) for b in range(streams)]
+        rt.reset()
+        mean, per = rt.device_run(events)
+        assert mean > 0 and per.shape == (steps,) and np.all(per > 0)
+        for b in range(streams):
+            traced = rt.snapshot(b)
+            assert traced[0] == states[b][0] == steps
+            for x, y in zip(traced[1:], states[b][1:]):
+                np.testing.assert_array_equal(x, y)
+        # the scores of the last device-run step are the stepped ones
+        rt.reset()
+        for i in range(steps - 1):
+            rt.step(events[i])
+        np.testing.assert_array_equal(rt.step(events[-1]), stepped[-1])
+
+
+def test_invalid_arguments_are_rejected():
+    c = SHAPES['small']
+    w = synthetic_checkpoint(c, seed=15)
+    for streams in (0, 257):
+        with pytest.raises(RuntimeError, match='Streams'):
+            BatchRuntime((c, w, False), streams)
+    with pytest.raises(RuntimeError, match='FP32'):
+        BatchRuntime((c, synthetic_checkpoint(c, seed=15, mixed=True), True), 4)
+    odd = ModelConfig(1, 40, 1, 40, 8, 40)
+    with pytest.raises(RuntimeError, match='multiples of 16'):
+        BatchRuntime((odd, synthetic_checkpoint(odd, seed=15), False), 4)
+    with batch((c, w, False), 4) as rt:
+        with pytest.raises(RuntimeError, match='out of range'):
+            rt.reset(4)
+        with pytest.raises(RuntimeError, match='out of range'):
+            rt.snapshot(-1)
+        with pytest.raises(ValueError):
+            rt.step(np.zeros((3, c.features), dtype=np.float32))
