@@ -2,10 +2,10 @@
 // K/V ring, hidden state and position. One step advances every stream by one event. The
 // projections become skinny GEMMs [B x K] . W^T computed with MFMA (v_mfma_f32_16x16x4_f32:
 // FP32 operands, FP32 accumulation; bfloat16 weights are widened exactly), split over K
-// across workgroups so that small batches still spread the weight stream over the chip. A
-// reduce kernel per projection adds the K-slices in a fixed order and applies the phase's
-// epilogue (RoPE and ring write, residual, SwiGLU). Activations, K/V and reductions are FP32,
-// so each stream follows the single-stream runtime's arithmetic up to summation order.
+// across the waves of a workgroup and summed in LDS in a fixed order, with the RMSNorm in the
+// prologue and the phase's epilogue (RoPE and ring write, residual, SwiGLU) fused. Activations,
+// K/V and reductions are FP32, so each stream follows the single-stream runtime's arithmetic
+// up to summation order.
 #pragma once
 
 #include "step_device.hpp"
@@ -18,9 +18,9 @@ constexpr int kBatchTile = 16;   // MFMA rows
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 struct BatchArgs {
-  int streams, streams_p;  // B and B rounded up to 16
+  int streams, streams_p;  // B and the padded batch (16, 32 or a multiple of 64)
   int layers, width, heads, dim, ffn, window, features;
-  int width_p, ffn_p, features_p, xcols;  // padded row lengths; xcols = widest GEMM input
+  int width_p, ffn_p, features_p;  // padded row lengths
   float epsilon;
   const char* weights;
   uint32_t w_input, w_final_norm, w_score;
@@ -32,11 +32,9 @@ struct BatchArgs {
   unsigned long long* position;    // [B]
   float* in;                       // [Bp][features_p] events
   float* x;                        // [Bp][width_p] residual stream
-  float* xn;                       // [Bp][xcols] normalized x, then the GEMM input
   float* attn;                     // [Bp][width_p] attention output
   float* act;                      // [Bp][ffn_p] SwiGLU output
   float* q;                        // [Bp][width] rotated queries
-  float* part;                     // split-K partial sums [ks][Bp][N]
   float* score;                    // [B]
 };
 
@@ -53,149 +51,164 @@ __device__ __forceinline__ float4 load_w4(const char* w, uint32_t woff, int row,
   }
 }
 
-// part[ks][b][n] = sum over k in K-slice ks of X[b][k] * W[n][k], for the 16 columns of this
-// workgroup and every batch tile. One wave per workgroup; grid (N / 16, slices).
-// MFMA 16x16x4 layout: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16]; register r
-// of lane l holds D[4 (l / 16) + r][l % 16]. The four MFMA steps of a 16-wide k block use
-// k = kb + 4 (l / 16) + c for step c, the same index for A and B.
-template <int P>
-__global__ __launch_bounds__(64) void batch_gemm(const BatchArgs* __restrict__ ap, const float* __restrict__ X, int ldx,
-                                                 uint32_t woff, int ldw, int N, int K, int kc,
-                                                 float* __restrict__ part) {
-  const BatchArgs& a = *ap;
-  const int lane = threadIdx.x;
-  const int n0 = blockIdx.x * kBatchTile;
-  const int ks = blockIdx.y;
-  const int k0 = ks * kc;
-  const int k1 = k0 + kc < K ? k0 + kc : K;
-  const int tiles = a.streams_p / kBatchTile;
-  const int r16 = lane & 15, g = lane >> 4;
-  f4v acc[kBatchMax / kBatchTile];
-#pragma unroll
-  for (int t = 0; t < kBatchMax / kBatchTile; t++) acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
-  for (int kb = k0; kb < k1; kb += 16) {
-    const float4 w = load_w4<P>(a.weights, woff, n0 + r16, ldw, kb + 4 * g);
-#pragma unroll
-    for (int t = 0; t < kBatchMax / kBatchTile; t++) {
-      if (t < tiles) {
-        const float4 xv = *reinterpret_cast<const float4*>(X + (size_t)(t * kBatchTile + r16) * ldx + kb + 4 * g);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, w.x, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, w.y, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.z, w.z, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.w, w.w, acc[t], 0, 0, 0);
-      }
-    }
-  }
-  float* out = part + (size_t)ks * a.streams_p * N;
-#pragma unroll
-  for (int t = 0; t < kBatchMax / kBatchTile; t++)
-    if (t < tiles)
-#pragma unroll
-      for (int r = 0; r < 4; r++) out[(size_t)(t * kBatchTile + 4 * g + r) * N + n0 + r16] = acc[t][r];
-}
-
-// Sum of the K-slices of output (b, n), in slice order.
-__device__ __forceinline__ float slice_sum(const float* part, int slices, int rows, int N, int b, int n) {
-  float s = part[(size_t)b * N + n];
-  for (int ks = 1; ks < slices; ks++) s += part[((size_t)ks * rows + b) * N + n];
-  return s;
-}
+constexpr int kProjWaves = 8;    // K-slices of a projection workgroup, one per wave
+constexpr int kGroupTiles = 4;   // most batch tiles (16 streams each) per projection workgroup
 
 enum BatchEpilogue : int { kEpInput = 0, kEpQkv, kEpOut, kEpGateUp, kEpDown };
 
-// Reduce the K-slices of one projection and apply its epilogue; one thread per output unit
-// (a row, or the row pair of a RoPE pair / gate-up pair) of a stream below B.
-template <int E>
-__global__ __launch_bounds__(256) void batch_reduce(const BatchArgs* __restrict__ ap, int layer, int N, int slices) {
+// One projection Y = X . W^T over the batch, with its phase's epilogue. Workgroup
+// (column tile of 16 outputs, group of NT batch tiles); each of its 8 waves takes one
+// K-slice of K / 8 columns and accumulates the group's tiles with v_mfma_f32_16x16x4_f32.
+// The slices are summed in LDS in wave order, so a stream's outputs depend only on its own
+// row (bit-identical for any batch size and grouping). The padded batch is a multiple of NT
+// tiles, so the loop has no branches and the compiler keeps several k blocks of loads in
+// flight.
+// MFMA 16x16x4 layout: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16]; register r
+// of lane l holds D[4 (l / 16) + r][l % 16]. The four MFMA steps of a 16-wide k block use
+// k = kb + 4 (l / 16) + c for step c, the same index for A and B.
+// kNorm: X is the residual stream x and the projection consumes RMSNorm(x) . g
+// (src/cuda/Primitives.cuh:122-135). The waves feed x * g to the MFMAs, accumulate the row's
+// sum of squares from the same loads, and the epilogue scales the row by
+// 1 / sqrt(sum / d + eps).
+template <int P, int E, bool kNorm, int NT>
+__global__ __launch_bounds__(512) void batch_proj(const BatchArgs* __restrict__ ap, const float* __restrict__ X, int ldx,
+                                                  uint32_t woff, int ldw, int N, int K, uint32_t w_norm, int layer) {
   const BatchArgs& a = *ap;
-  const int unit = (E == kEpQkv || E == kEpGateUp) ? 2 : 1;
-  const int units = N / unit;
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= a.streams * units) return;
-  const int b = idx / units, u = idx - b * units;
-  const int n = u * unit;
-  const float s0 = slice_sum(a.part, slices, a.streams_p, N, b, n);
-  const float s1 = unit == 2 ? slice_sum(a.part, slices, a.streams_p, N, b, n + 1) : 0.f;
-  float* xb = a.x + (size_t)b * a.width_p;
-  if constexpr (E == kEpInput) {
-    xb[n] = s0;
-  } else if constexpr (E == kEpQkv) {
-    // src/cuda/Primitives.cuh:148-166: RoPE on adjacent pairs of q and k, then the ring write.
-    const int sec = (n >= a.width) + (n >= 2 * a.width);
-    const int i = n - sec * a.width;
-    const unsigned long long t = a.position[b];
-    float va = s0, vb = s1;
-    if (sec < 2) {
-      const int e = i % a.dim;
-      const float angle = (float)t * a.rope_freq[e >> 1];
-      const float co = cosf(angle), si = sinf(angle);
-      const float ra = va * co - vb * si, rb = va * si + vb * co;
-      va = ra;
-      vb = rb;
-    }
-    if (sec == 0) {
-      a.q[(size_t)b * a.width + i] = va;
-      a.q[(size_t)b * a.width + i + 1] = vb;
-    } else {
-      const int h = i / a.dim, d = i - h * a.dim;
-      const int slot = (int)(t % (unsigned long long)a.window);
-      const size_t ring = ((((size_t)b * a.layers + layer) * a.heads + h) * a.window + slot) * a.dim + d;
-      float* dst = sec == 1 ? a.keys : a.values;
-      dst[ring] = va;
-      dst[ring + 1] = vb;
-    }
-  } else if constexpr (E == kEpOut) {
-    xb[n] = xb[n] + s0;
-  } else if constexpr (E == kEpGateUp) {
-    a.act[(size_t)b * a.ffn_p + u] = (s0 / (1.0f + expf(-s0))) * s1;
-  } else {
-    const float v = xb[n] + s0;
-    xb[n] = v;
-    a.hidden[((size_t)b * a.layers + layer) * a.width + n] = v;
+  __shared__ float red[kProjWaves][NT][16][17];
+  __shared__ float sq[kProjWaves][NT][16];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n0 = blockIdx.x * kBatchTile;
+  const int t0 = blockIdx.y * NT;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int slice = K / kProjWaves;
+  const int k0 = wave * slice, k1 = k0 + slice;
+  f4v acc[NT];
+  float ss[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
+    ss[t] = 0.f;
   }
-}
-
-// RMSNorm of every stream's x into xn (src/cuda/Primitives.cuh:122-135); padding columns and
-// padding streams are zero. One workgroup per row of the padded batch.
-template <int P>
-__global__ __launch_bounds__(256) void batch_norm(const BatchArgs* __restrict__ ap, uint32_t w_norm) {
-  const BatchArgs& a = *ap;
-  __shared__ float red[4];
-  const int b = blockIdx.x;
-  const float* xb = a.x + (size_t)b * a.width_p;
-  float* out = a.xn + (size_t)b * a.xcols;
-  if (b >= a.streams) {
-    for (int i = threadIdx.x; i < a.width_p; i += blockDim.x) out[i] = 0.f;
-    return;
+  const float* xr = X + (size_t)(t0 * kBatchTile + r16) * ldx + 4 * g;
+#pragma unroll 4
+  for (int kb = k0; kb < k1; kb += 16) {
+    const float4 w = load_w4<P>(a.weights, woff, n0 + r16, ldw, kb + 4 * g);
+    // The norm vector holds `width` values (a multiple of 16): a group of 4 is all in or all out.
+    float4 gn = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (kNorm)
+      if (kb + 4 * g < a.width) gn = load_w4<P>(a.weights, w_norm, 0, 0, kb + 4 * g);
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      float4 xv = *reinterpret_cast<const float4*>(xr + (size_t)t * kBatchTile * ldx + kb);
+      if constexpr (kNorm) {
+        ss[t] += xv.x * xv.x;
+        ss[t] += xv.y * xv.y;
+        ss[t] += xv.z * xv.z;
+        ss[t] += xv.w * xv.w;
+        xv.x *= gn.x;
+        xv.y *= gn.y;
+        xv.z *= gn.z;
+        xv.w *= gn.w;
+      }
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, w.x, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, w.y, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.z, w.z, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.w, w.w, acc[t], 0, 0, 0);
+    }
   }
-  float s = 0.f;
-  for (int i = threadIdx.x; i < a.width; i += blockDim.x) s += xb[i] * xb[i];
-  s = wave_total(s);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) red[wave][t][4 * g + r][r16] = acc[t][r];
+    if constexpr (kNorm) {
+      const float v = column_sum(ss[t], 16);
+      if (g == 0) sq[wave][t][r16] = v;
+    }
+  }
   __syncthreads();
-  const float sum = (red[0] + red[1]) + (red[2] + red[3]);
-  const float scale = 1.0f / sqrtf(sum / (float)a.width + a.epsilon);
-  for (int i = threadIdx.x; i < a.width_p; i += blockDim.x) {
-    float v = 0.f;
-    if (i < a.width) {
-      const float w = P == kFp32 ? reinterpret_cast<const float*>(a.weights + w_norm)[i]
-                                 : __builtin_bit_cast(float, (unsigned)reinterpret_cast<const unsigned short*>(a.weights + w_norm)[i] << 16);
-      v = xb[i] * scale * w;
+  // Epilogue: one thread per output unit (a column, or the column pair of a RoPE pair /
+  // gate-up pair) of a stream below B.
+  constexpr int unit = (E == kEpQkv || E == kEpGateUp) ? 2 : 1;
+  constexpr int per_row = kBatchTile / unit;
+  for (int o = threadIdx.x; o < NT * kBatchTile * per_row; o += blockDim.x) {
+    const int t = o / (kBatchTile * per_row);
+    const int row = (o / per_row) % kBatchTile;
+    const int c = (o % per_row) * unit;
+    const int b = (t0 + t) * kBatchTile + row;
+    if (b >= a.streams) continue;
+    float s0 = red[0][t][row][c], s1 = unit == 2 ? red[0][t][row][c + 1] : 0.f;
+#pragma unroll
+    for (int w = 1; w < kProjWaves; w++) {
+      s0 += red[w][t][row][c];
+      if (unit == 2) s1 += red[w][t][row][c + 1];
     }
-    out[i] = v;
+    if constexpr (kNorm) {
+      float sum = sq[0][t][row];
+#pragma unroll
+      for (int w = 1; w < kProjWaves; w++) sum += sq[w][t][row];
+      const float scale = 1.0f / sqrtf(sum / (float)a.width + a.epsilon);
+      s0 *= scale;
+      s1 *= scale;
+    }
+    const int n = n0 + c;
+    float* xb = a.x + (size_t)b * a.width_p;
+    if constexpr (E == kEpInput) {
+      xb[n] = s0;
+    } else if constexpr (E == kEpQkv) {
+      // src/cuda/Primitives.cuh:148-166: RoPE on adjacent pairs of q and k, then the ring write.
+      const int sec = (n >= a.width) + (n >= 2 * a.width);
+      const int i = n - sec * a.width;
+      const unsigned long long pos = a.position[b];
+      float va = s0, vb = s1;
+      if (sec < 2) {
+        const int e = i % a.dim;
+        const float angle = (float)pos * a.rope_freq[e >> 1];
+        const float co = cosf(angle), si = sinf(angle);
+        const float ra = va * co - vb * si, rb = va * si + vb * co;
+        va = ra;
+        vb = rb;
+      }
+      if (sec == 0) {
+        a.q[(size_t)b * a.width + i] = va;
+        a.q[(size_t)b * a.width + i + 1] = vb;
+      } else {
+        const int h = i / a.dim, d = i - h * a.dim;
+        const int slot = (int)(pos % (unsigned long long)a.window);
+        const size_t ring = ((((size_t)b * a.layers + layer) * a.heads + h) * a.window + slot) * a.dim + d;
+        float* dst = sec == 1 ? a.keys : a.values;
+        dst[ring] = va;
+        dst[ring + 1] = vb;
+      }
+    } else if constexpr (E == kEpOut) {
+      xb[n] = xb[n] + s0;
+    } else if constexpr (E == kEpGateUp) {
+      a.act[(size_t)b * a.ffn_p + (n >> 1)] = (s0 / (1.0f + expf(-s0))) * s1;
+    } else {
+      const float v = xb[n] + s0;
+      xb[n] = v;
+      a.hidden[((size_t)b * a.layers + layer) * a.width + n] = v;
+    }
   }
 }
 
 // Attention of one (stream, head) over the stream's valid ring slots [0, valid)
-// (src/cuda/Primitives.cuh:167-219): logits q.K/sqrt(dh), softmax, weighted V. One wave per
-// workgroup: lane s computes the logits of slots s, s + 64, ... (a K row each, 16 bytes at a
-// time); the probabilities go through LDS (dynamic, `window` floats) to the lanes that sum V
-// by output coordinate.
-__global__ __launch_bounds__(64) void batch_attention(const BatchArgs* __restrict__ ap, int layer) {
+// (src/cuda/Primitives.cuh:167-219): logits q.K/sqrt(dh), softmax, weighted V. Slot order does
+// not change the result beyond summation order. Four waves; every load is a coalesced row:
+//  - logits: 16 lanes per K row (16 bytes each, rows of up to 64 FP32 per pass), a 16-lane
+//    DPP sum, so a wave covers 4 rows per load;
+//  - softmax: workgroup max and sum through LDS;
+//  - values: lane group (slot s mod 16) accumulates its slots' V rows, 16 bytes per lane, and
+//    the 16 groups are summed in LDS in group order.
+// Needs dh a multiple of 4; dynamic LDS holds `window` floats of probabilities.
+constexpr int kAttnThreads = 256;
+__global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs* __restrict__ ap, int layer) {
   const BatchArgs& a = *ap;
   extern __shared__ float pr[];
+  __shared__ float wred[kAttnThreads / 64];
+  __shared__ float4 vred[16][17];
   const int b = blockIdx.x / a.heads, h = blockIdx.x - b * a.heads;
-  const int lane = threadIdx.x, dim = a.dim;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int dim = a.dim, r = tid & 15, grp = tid >> 4;  // 16 groups of 16 lanes
   const unsigned long long t = a.position[b];
   const int valid = t + 1 < (unsigned long long)a.window ? (int)(t + 1) : a.window;
   const size_t base = (((size_t)b * a.layers + layer) * a.heads + h) * (size_t)a.window * dim;
@@ -204,38 +217,73 @@ __global__ __launch_bounds__(64) void batch_attention(const BatchArgs* __restric
   const float* q = a.q + (size_t)b * a.width + h * dim;
   const float div = sqrtf((float)dim);
   float mx = -INFINITY;
-  for (int s = lane; s < valid; s += 64) {
-    const float* kr = K + (size_t)s * dim;
+  for (int s0 = 0; s0 < valid; s0 += kAttnThreads / 16) {
+    const int s = s0 + grp;
     float dot = 0.f;
-    if ((dim & 3) == 0) {
-      for (int d = 0; d < dim; d += 4) {
-        const float4 kv = *reinterpret_cast<const float4*>(kr + d);
-        dot += q[d] * kv.x;
-        dot += q[d + 1] * kv.y;
-        dot += q[d + 2] * kv.z;
-        dot += q[d + 3] * kv.w;
+    if (s < valid) {
+      for (int d = 4 * r; d < dim; d += 64) {
+        const float4 kv = *reinterpret_cast<const float4*>(K + (size_t)s * dim + d);
+        const float4 qv = *reinterpret_cast<const float4*>(q + d);
+        dot += qv.x * kv.x;
+        dot += qv.y * kv.y;
+        dot += qv.z * kv.z;
+        dot += qv.w * kv.w;
       }
-    } else {
-      for (int d = 0; d < dim; d++) dot += q[d] * kr[d];
     }
-    const float lg = dot / div;
-    pr[s] = lg;
-    mx = fmaxf(mx, lg);
+    dot = group_sum(dot, 16);
+    if (s < valid) {
+      const float lg = dot / div;
+      if (r == 0) pr[s] = lg;
+      mx = fmaxf(mx, lg);
+    }
   }
   mx = wave_top(mx);
+  if (lane == 0) wred[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
   float sum = 0.f;
-  for (int s = lane; s < valid; s += 64) {
+  for (int s = tid; s < valid; s += kAttnThreads) {
     const float e = expf(pr[s] - mx);
     pr[s] = e;
     sum += e;
   }
   sum = wave_total(sum);
+  __syncthreads();  // every wave has read wred (max) and written its probabilities
+  if (lane == 0) wred[wave] = sum;
   __syncthreads();
+  sum = (wred[0] + wred[1]) + (wred[2] + wred[3]);
   float* out = a.attn + (size_t)b * a.width_p + h * dim;
-  for (int d = lane; d < dim; d += 64) {
-    float o = 0.f;
-    for (int s = 0; s < valid; s++) o += pr[s] * V[(size_t)s * dim + d];
-    out[d] = o / sum;
+  for (int d0 = 0; d0 < dim; d0 += 64) {
+    const int d = d0 + 4 * r;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (d < dim) {
+      for (int s = grp; s < valid; s += 16) {
+        const float p = pr[s];
+        const float4 vv = *reinterpret_cast<const float4*>(V + (size_t)s * dim + d);
+        o.x += p * vv.x;
+        o.y += p * vv.y;
+        o.z += p * vv.z;
+        o.w += p * vv.w;
+      }
+    }
+    vred[grp][r] = o;
+    __syncthreads();
+    if (tid < 16 && d0 + 4 * tid < dim) {
+      float4 acc = vred[0][tid];
+      for (int k = 1; k < 16; k++) {
+        const float4 v = vred[k][tid];
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+      }
+      float* od = out + d0 + 4 * tid;
+      od[0] = acc.x / sum;
+      od[1] = acc.y / sum;
+      od[2] = acc.z / sum;
+      od[3] = acc.w / sum;
+    }
+    __syncthreads();
   }
 }
 

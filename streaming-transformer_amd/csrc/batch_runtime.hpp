@@ -1,8 +1,8 @@
 // Host side of the batched runtime (included by runtime.hip, inside namespace stamd): B
-// independent streams over one weight arena. A step is a fixed kernel sequence captured once
-// in a hipGraph: input projection, then per layer norm, QKV (+RoPE, ring write), attention,
-// OUT (+residual), norm, gate/up (+SwiGLU), down (+residual, hidden), then the final norm and
-// the scores. Each projection is a split-K MFMA GEMM followed by its reduce/epilogue kernel.
+// independent streams over one weight arena. A step is a fixed sequence of 5L + 2 kernels
+// captured once in a hipGraph: the input projection, then per layer QKV (RMSNorm prologue,
+// RoPE and ring-write epilogue), attention, OUT (+residual), gate/up (RMSNorm prologue,
+// SwiGLU epilogue), down (+residual, hidden), then the final norm and the scores.
 #pragma once
 
 class Batch {
@@ -16,20 +16,10 @@ class Batch {
 
  private:
   template <int P> void launch_sequence();
+  int group_tiles(int N) const;
   void launch() {
     if (prec_ == kFp32) launch_sequence<kFp32>();
     else launch_sequence<kBf16w>();
-  }
-  // K-slices of a projection with K columns: enough workgroups to spread the weight stream
-  // (about 512 over N / 16 column tiles), each slice a multiple of 16 columns.
-  void slices(int N, int K, int& ks, int& kc) const {
-    const int tiles = N / kBatchTile;
-    int want = (512 + tiles - 1) / tiles;
-    const int blocks16 = K / 16;
-    if (want > blocks16) want = blocks16;
-    if (want < 1) want = 1;
-    kc = (blocks16 + want - 1) / want * 16;
-    ks = (K + kc - 1) / kc;
   }
   void sync() { HIP_CHECK(hipStreamSynchronize(stream_)); }
 
@@ -38,8 +28,7 @@ class Batch {
   hipStream_t stream_ = nullptr;
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;
-  DeviceBuffer weights_, keys_, values_, hidden_, position_, in_, x_, xn_, attn_, act_, q_, part_, score_, rope_,
-      args_dev_;
+  DeviceBuffer weights_, keys_, values_, hidden_, position_, in_, x_, attn_, act_, q_, score_, rope_, args_dev_;
   PinnedBuffer host_in_, host_out_;
   StepArgs offsets_{};  // weight arena offsets (shared layout with the single-stream runtime)
   BatchArgs args_{};
@@ -57,8 +46,11 @@ Batch::Batch(const st_config& config, const st_tensor* tensors, size_t count, in
     throw Error(ST_ERR_INVALID, "Batched streams need width and 2*ffn to be multiples of 16");
   prec_ = weight_dtype == ST_WEIGHTS_BF16 ? kBf16w : kFp32;
   streams_ = streams;
-  streams_p_ = (streams + kBatchTile - 1) / kBatchTile * kBatchTile;
+  // Padded batch: 16 or 32 rows, else a multiple of 64, so that every projection's batch
+  // groups (1, 2 or 4 tiles of 16) divide it.
+  streams_p_ = streams <= 16 ? 16 : streams <= 32 ? 32 : (streams + 63) / 64 * 64;
   dim_ = c_.width / c_.heads;
+  if (dim_ % 4) throw Error(ST_ERR_INVALID, "Batched streams need a head dimension that is a multiple of 4");
   int device = 0;
   HIP_CHECK(hipGetDevice(&device));
   hipDeviceProp_t prop;
@@ -87,7 +79,6 @@ Batch::Batch(const st_config& config, const st_tensor* tensors, size_t count, in
   a.width_p = offsets_.width_p;
   a.ffn_p = offsets_.ffn_p;
   a.features_p = offsets_.features_p;
-  a.xcols = std::max({a.width_p, a.ffn_p, a.features_p});
   a.epsilon = c_.epsilon;
   a.weights = offsets_.weights;
   a.w_input = offsets_.w_input;
@@ -115,21 +106,10 @@ Batch::Batch(const st_config& config, const st_tensor* tensors, size_t count, in
   a.position = reinterpret_cast<unsigned long long*>(position_.ptr);
   a.in = zeroed(in_, (size_t)streams_p_ * a.features_p);
   a.x = zeroed(x_, (size_t)streams_p_ * a.width_p);
-  a.xn = zeroed(xn_, (size_t)streams_p_ * a.xcols);
   a.attn = zeroed(attn_, (size_t)streams_p_ * a.width_p);
   a.act = zeroed(act_, (size_t)streams_p_ * a.ffn_p);
   a.q = zeroed(q_, (size_t)streams_p_ * a.width);
   a.score = zeroed(score_, (size_t)streams_);
-  // Split-K partials: the largest slices x Bp x N over the projections.
-  size_t part = 0;
-  const int shapes[5][2] = {{c_.width, a.features_p}, {3 * c_.width, a.width_p}, {c_.width, a.width_p},
-                            {2 * c_.ffn, a.width_p}, {c_.width, a.ffn_p}};
-  for (auto& sh : shapes) {
-    int ks, kc;
-    slices(sh[0], sh[1], ks, kc);
-    part = std::max(part, (size_t)ks * streams_p_ * sh[0]);
-  }
-  a.part = zeroed(part_, part);
   host_in_.alloc((size_t)streams_p_ * a.features_p * 4);
   std::memset(host_in_.ptr, 0, (size_t)streams_p_ * a.features_p * 4);
   host_out_.alloc((size_t)streams_ * 4);
@@ -155,38 +135,39 @@ Batch::~Batch() {
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
+// Batch tiles per projection workgroup: the largest of 4, 2, 1 that still gives at least 256
+// workgroups (one per CU), so that narrow projections at small batches spread over the chip.
+int Batch::group_tiles(int N) const {
+  const int tiles = streams_p_ / kBatchTile, cols = N / kBatchTile;
+  for (int nt = kGroupTiles; nt > 1; nt >>= 1)
+    if (tiles % nt == 0 && cols * (tiles / nt) >= 256) return nt;
+  return 1;
+}
+
 template <int P>
 void Batch::launch_sequence() {
   const BatchArgs& a = args_;
-  auto gemm = [&](const float* X, int ldx, uint32_t woff, int ldw, int N, int K) {
-    int ks, kc;
-    slices(N, K, ks, kc);
-    hipLaunchKernelGGL(batch_gemm<P>, dim3(N / kBatchTile, ks), dim3(64), 0, stream_, dargs_, X, ldx, woff, ldw, N, K,
-                       kc, a.part);
-    return ks;
+  const int tiles = streams_p_ / kBatchTile;
+  auto proj = [&](auto k1, auto k2, auto k4, const float* X, int ld, uint32_t woff, int N, uint32_t norm, int layer) {
+    const int nt = group_tiles(N);
+    const dim3 grid(N / kBatchTile, tiles / nt), block(64 * kProjWaves);
+    if (nt == 4) hipLaunchKernelGGL(k4, grid, block, 0, stream_, dargs_, X, ld, woff, ld, N, ld, norm, layer);
+    else if (nt == 2) hipLaunchKernelGGL(k2, grid, block, 0, stream_, dargs_, X, ld, woff, ld, N, ld, norm, layer);
+    else hipLaunchKernelGGL(k1, grid, block, 0, stream_, dargs_, X, ld, woff, ld, N, ld, norm, layer);
   };
-  auto reduce = [&](auto kernel, int layer, int N, int ks, int unit) {
-    const int threads = streams_ * (N / unit);
-    hipLaunchKernelGGL(kernel, dim3((threads + 255) / 256), dim3(256), 0, stream_, dargs_, layer, N, ks);
-  };
+#define STAMD_PROJ(E, NORM) batch_proj<P, E, NORM, 1>, batch_proj<P, E, NORM, 2>, batch_proj<P, E, NORM, 4>
   const int d = c_.width, F = c_.ffn;
-  int ks = gemm(a.in, a.features_p, a.w_input, a.features_p, d, a.features_p);
-  reduce(batch_reduce<kEpInput>, 0, d, ks, 1);
+  proj(STAMD_PROJ(kEpInput, false), a.in, a.features_p, a.w_input, d, 0u, 0);
   for (int l = 0; l < c_.layers; l++) {
     const LayerWeights& w = a.layer[l];
-    hipLaunchKernelGGL(batch_norm<P>, dim3(streams_p_), dim3(256), 0, stream_, dargs_, w.norm1);
-    ks = gemm(a.xn, a.xcols, w.qkv, a.width_p, 3 * d, a.width_p);
-    reduce(batch_reduce<kEpQkv>, l, 3 * d, ks, 2);
-    hipLaunchKernelGGL(batch_attention, dim3(streams_ * c_.heads), dim3(64), (size_t)c_.window * 4, stream_, dargs_,
-                       l);
-    ks = gemm(a.attn, a.width_p, w.out, a.width_p, d, a.width_p);
-    reduce(batch_reduce<kEpOut>, l, d, ks, 1);
-    hipLaunchKernelGGL(batch_norm<P>, dim3(streams_p_), dim3(256), 0, stream_, dargs_, w.norm2);
-    ks = gemm(a.xn, a.xcols, w.gateup, a.width_p, 2 * F, a.width_p);
-    reduce(batch_reduce<kEpGateUp>, l, 2 * F, ks, 2);
-    ks = gemm(a.act, a.ffn_p, w.down, a.ffn_p, d, a.ffn_p);
-    reduce(batch_reduce<kEpDown>, l, d, ks, 1);
+    proj(STAMD_PROJ(kEpQkv, true), a.x, a.width_p, w.qkv, 3 * d, w.norm1, l);
+    hipLaunchKernelGGL(batch_attention, dim3(streams_ * c_.heads), dim3(kAttnThreads), (size_t)c_.window * 4, stream_,
+                       dargs_, l);
+    proj(STAMD_PROJ(kEpOut, false), a.attn, a.width_p, w.out, d, 0u, l);
+    proj(STAMD_PROJ(kEpGateUp, true), a.x, a.width_p, w.gateup, 2 * F, w.norm2, l);
+    proj(STAMD_PROJ(kEpDown, false), a.act, a.ffn_p, w.down, d, 0u, l);
   }
+#undef STAMD_PROJ
   hipLaunchKernelGGL(batch_final<P>, dim3(streams_), dim3(64), 0, stream_, dargs_);
   HIP_CHECK(hipGetLastError());
 }
