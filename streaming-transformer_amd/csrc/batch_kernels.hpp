@@ -16,6 +16,7 @@ constexpr int kBatchMax = 256;   // streams per batch (16 batch tiles of 16 in t
 constexpr int kBatchTile = 16;   // MFMA rows
 
 typedef float f4v __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 struct BatchArgs {
   int streams, streams_p;  // B and the padded batch (16, 32 or a multiple of 64)
@@ -37,19 +38,6 @@ struct BatchArgs {
   float* q;                        // [Bp][width] rotated queries
   float* score;                    // [B]
 };
-
-// Four consecutive weights of row `row` from column `k` (FP32 or bfloat16 storage).
-template <int P>
-__device__ __forceinline__ float4 load_w4(const char* w, uint32_t woff, int row, int ldw, int k) {
-  const uint32_t e = (uint32_t)row * (uint32_t)ldw + (uint32_t)k;
-  if constexpr (P == kFp32) {
-    return *reinterpret_cast<const float4*>(w + woff + e * 4u);
-  } else {
-    const uint2 u = *reinterpret_cast<const uint2*>(w + woff + e * 2u);
-    return make_float4(__builtin_bit_cast(float, u.x << 16), __builtin_bit_cast(float, u.x & 0xffff0000u),
-                       __builtin_bit_cast(float, u.y << 16), __builtin_bit_cast(float, u.y & 0xffff0000u));
-  }
-}
 
 constexpr int kProjWaves = 8;    // K-slices of a projection workgroup, one per wave
 constexpr int kGroupTiles = 4;   // most batch tiles (16 streams each) per projection workgroup
@@ -89,31 +77,129 @@ __global__ __launch_bounds__(512) void batch_proj(const BatchArgs* __restrict__ 
     acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
     ss[t] = 0.f;
   }
-  const float* xr = X + (size_t)(t0 * kBatchTile + r16) * ldx + 4 * g;
-#pragma unroll 4
-  for (int kb = k0; kb < k1; kb += 16) {
-    const float4 w = load_w4<P>(a.weights, woff, n0 + r16, ldw, kb + 4 * g);
-    // The norm vector holds `width` values (a multiple of 16): a group of 4 is all in or all out.
-    float4 gn = make_float4(0.f, 0.f, 0.f, 0.f);
-    if constexpr (kNorm)
-      if (kb + 4 * g < a.width) gn = load_w4<P>(a.weights, w_norm, 0, 0, kb + 4 * g);
+  if constexpr (P == kFp32) {
+    // k block of 16: four v_mfma_f32_16x16x4_f32; lane (r16, g) holds k = kb + 4 g .. + 3.
+    const float* xr = X + (size_t)(t0 * kBatchTile + r16) * ldx + 4 * g;
+    const float* wr = reinterpret_cast<const float*>(a.weights + woff) + (size_t)(n0 + r16) * ldw + 4 * g;
+    const float* gr = reinterpret_cast<const float*>(a.weights + w_norm) + 4 * g;
+    auto load = [&](int kb, float4& w, float4& gn, float4* xv) {
+      w = *reinterpret_cast<const float4*>(wr + kb);
+      // The norm vector holds `width` values (a multiple of 16): a group of 4 is all in or out.
+      gn = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (kNorm)
+        if (kb + 4 * g < a.width) gn = *reinterpret_cast<const float4*>(gr + kb);
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-      float4 xv = *reinterpret_cast<const float4*>(xr + (size_t)t * kBatchTile * ldx + kb);
-      if constexpr (kNorm) {
-        ss[t] += xv.x * xv.x;
-        ss[t] += xv.y * xv.y;
-        ss[t] += xv.z * xv.z;
-        ss[t] += xv.w * xv.w;
-        xv.x *= gn.x;
-        xv.y *= gn.y;
-        xv.z *= gn.z;
-        xv.w *= gn.w;
+      for (int t = 0; t < NT; t++) xv[t] = *reinterpret_cast<const float4*>(xr + (size_t)t * kBatchTile * ldx + kb);
+    };
+    float4 w, gn, xv[NT];
+    load(k0, w, gn, xv);
+    for (int kb = k0; kb < k1; kb += 16) {
+      // Issue the next block's loads before this block's MFMAs (the last block reloads itself).
+      float4 w2, gn2, xv2[NT];
+      load(kb + 16 < k1 ? kb + 16 : kb, w2, gn2, xv2);
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        float4 x = xv[t];
+        if constexpr (kNorm) {
+          ss[t] += x.x * x.x;
+          ss[t] += x.y * x.y;
+          ss[t] += x.z * x.z;
+          ss[t] += x.w * x.w;
+          x.x *= gn.x;
+          x.y *= gn.y;
+          x.z *= gn.z;
+          x.w *= gn.w;
+        }
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, w.x, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, w.y, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, w.z, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, w.w, acc[t], 0, 0, 0);
       }
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, w.x, acc[t], 0, 0, 0);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, w.y, acc[t], 0, 0, 0);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.z, w.z, acc[t], 0, 0, 0);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.w, w.w, acc[t], 0, 0, 0);
+      w = w2;
+      gn = gn2;
+#pragma unroll
+      for (int t = 0; t < NT; t++) xv[t] = xv2[t];
+    }
+  } else {
+    // bfloat16 weights: k block of 32 on v_mfma_f32_16x16x32_bf16. The FP32 activation is
+    // split exactly into three bfloat16 terms, x = hi + mid + lo (truncations: hi keeps the
+    // top 8 significand bits, mid the next 8 of the remainder, lo the rest, at most 8 bits),
+    // and each term times the bfloat16 weight is exact in the FP32 accumulator, so the
+    // product is the FP32 path's up to accumulation order. Lane (r16, g) holds
+    // k = kb + 8 g .. + 7 for both operands; the sum over k does not depend on how the
+    // hardware orders the lane groups.
+    const float* xr = X + (size_t)(t0 * kBatchTile + r16) * ldx + 8 * g;
+    const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.weights + woff) + (size_t)(n0 + r16) * ldw + 8 * g;
+    const uint16_t* gr = reinterpret_cast<const uint16_t*>(a.weights + w_norm) + 8 * g;
+    struct X8 {
+      float4 lo, hi;
+    };
+    auto load = [&](int kb, uint4& w, uint4& gn, X8* xv) {
+      w = *reinterpret_cast<const uint4*>(wr + kb);
+      gn = make_uint4(0u, 0u, 0u, 0u);
+      if constexpr (kNorm)
+        if (kb + 8 * g < a.width) gn = *reinterpret_cast<const uint4*>(gr + kb);
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const float* p = xr + (size_t)t * kBatchTile * ldx + kb;
+        xv[t].lo = *reinterpret_cast<const float4*>(p);
+        xv[t].hi = *reinterpret_cast<const float4*>(p + 4);
+      }
+    };
+    uint4 w, gn;
+    X8 xv[NT];
+    load(k0, w, gn, xv);
+    for (int kb = k0; kb < k1; kb += 32) {
+      uint4 w2, gn2;
+      X8 xv2[NT];
+      load(kb + 32 < k1 ? kb + 32 : kb, w2, gn2, xv2);
+      const bf16x8 wb = __builtin_bit_cast(bf16x8, w);
+      float gv[8];
+      if constexpr (kNorm) {
+        const unsigned gu[4] = {gn.x, gn.y, gn.z, gn.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          gv[2 * i] = __builtin_bit_cast(float, gu[i] << 16);
+          gv[2 * i + 1] = __builtin_bit_cast(float, gu[i] & 0xffff0000u);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        float x[8] = {xv[t].lo.x, xv[t].lo.y, xv[t].lo.z, xv[t].lo.w, xv[t].hi.x, xv[t].hi.y, xv[t].hi.z, xv[t].hi.w};
+        if constexpr (kNorm) {
+#pragma unroll
+          for (int i = 0; i < 8; i++) {
+            ss[t] += x[i] * x[i];
+            x[i] *= gv[i];
+          }
+        }
+        unsigned ph[4], pm[4], pl[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          unsigned h2[2], m2[2], l2[2];
+#pragma unroll
+          for (int j = 0; j < 2; j++) {
+            const float v = x[2 * i + j];
+            const unsigned hb = __builtin_bit_cast(unsigned, v) & 0xffff0000u;
+            const float r1 = v - __builtin_bit_cast(float, hb);
+            const unsigned mb = __builtin_bit_cast(unsigned, r1) & 0xffff0000u;
+            const float r2 = r1 - __builtin_bit_cast(float, mb);
+            h2[j] = hb;
+            m2[j] = mb;
+            l2[j] = __builtin_bit_cast(unsigned, r2) & 0xffff0000u;
+          }
+          ph[i] = h2[1] | (h2[0] >> 16);
+          pm[i] = m2[1] | (m2[0] >> 16);
+          pl[i] = l2[1] | (l2[0] >> 16);
+        }
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ph), wb, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pm), wb, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pl), wb, acc[t], 0, 0, 0);
+      }
+      w = w2;
+      gn = gn2;
+#pragma unroll
+      for (int t = 0; t < NT; t++) xv[t] = xv2[t];
     }
   }
 #pragma unroll
@@ -217,18 +303,20 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
   const float* q = a.q + (size_t)b * a.width + h * dim;
   const float div = sqrtf((float)dim);
   float mx = -INFINITY;
+  // Rows past `valid` load row valid - 1 and are dropped, so the loop body has no branch
+  // around its loads and several passes of loads stay in flight.
+#pragma unroll 4
   for (int s0 = 0; s0 < valid; s0 += kAttnThreads / 16) {
     const int s = s0 + grp;
+    const float* kr = K + (size_t)(s < valid ? s : valid - 1) * dim;
     float dot = 0.f;
-    if (s < valid) {
-      for (int d = 4 * r; d < dim; d += 64) {
-        const float4 kv = *reinterpret_cast<const float4*>(K + (size_t)s * dim + d);
-        const float4 qv = *reinterpret_cast<const float4*>(q + d);
-        dot += qv.x * kv.x;
-        dot += qv.y * kv.y;
-        dot += qv.z * kv.z;
-        dot += qv.w * kv.w;
-      }
+    for (int d = 4 * r; d < dim; d += 64) {
+      const float4 kv = *reinterpret_cast<const float4*>(kr + d);
+      const float4 qv = *reinterpret_cast<const float4*>(q + d);
+      dot += qv.x * kv.x;
+      dot += qv.y * kv.y;
+      dot += qv.z * kv.z;
+      dot += qv.w * kv.w;
     }
     dot = group_sum(dot, 16);
     if (s < valid) {
@@ -257,6 +345,7 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
     const int d = d0 + 4 * r;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     if (d < dim) {
+#pragma unroll 4
       for (int s = grp; s < valid; s += 16) {
         const float p = pr[s];
         const float4 vv = *reinterpret_cast<const float4*>(V + (size_t)s * dim + d);
