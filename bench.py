@@ -12,8 +12,12 @@ launch per step, with a HIP event recorded on the runtime's stream after each la
 already resident in HBM). The library synchronizes its stream before and after the timed
 launches. One JSON line is printed.
 
+Secondary measurements (skipped with --quick) go under "extra": host-service latency through
+step(), the device loop, the persistent worker, and B independent streams over shared weights
+(Main, bfloat16 weights, W=128, B in 1, 16, 64, 256; --batched runs only that).
+
 Usage: python bench.py [--gpus 1] [--steps 1024] [--warmup 64] [--config large|main|small]
-                       [--precision fp32|bf16w|mixed] [--no-cpu-baseline] [--quick]
+                       [--precision fp32|bf16w|mixed] [--no-cpu-baseline] [--quick] [--batched]
 """
 from __future__ import annotations
 
@@ -32,7 +36,7 @@ for p in (ROOT, ROOT / 'streaming-transformer_amd'):
     if str(p) not in sys.path:
         sys.path.insert(0, str(p))
 
-from streamtx import Backend, ModelConfig, Runtime, RuntimeOptions, WeightStorage, synthetic_checkpoint  # noqa: E402
+from streamtx import Backend, BatchRuntime, ModelConfig, Runtime, RuntimeOptions, WeightStorage, synthetic_checkpoint  # noqa: E402
 
 CONFIGS = {
     'small': (ModelConfig(4, 256, 4, 1024, 64, 256), 0),
@@ -52,6 +56,29 @@ def weight_bytes_per_step(c: ModelConfig, wb: int) -> int:
 def kv_bytes_per_step(c: ModelConfig, kvb: int, valid: int) -> int:
     """K and V rows read over the valid window plus the new row written, every layer."""
     return 2 * c.layers * c.width * valid * kvb + 2 * c.layers * c.width * kvb
+
+
+def batched_streams(counts=(1, 16, 64, 256), steps=64):
+    """B independent streams over shared weights (st_batch_*): Main architecture with bfloat16
+    weights, W=128, as in the batched configuration. Each B runs a full window of events
+    (untimed), then `steps` timed steps with a HIP event after each. Algorithmic bytes per
+    step: the weights once plus every stream's K/V window and new rows (FP32)."""
+    c, seed = CONFIGS['main']
+    weights = synthetic_checkpoint(c, seed=seed)
+    out = {'workload': f'main bf16w batched streams, W={c.window}', 'steps': steps}
+    for b in counts:
+        rng = np.random.default_rng([seed, 2, b])
+        events = rng.standard_normal((c.window + steps, b, c.features), dtype=np.float32)
+        with BatchRuntime((c, weights, False), b, WeightStorage.BF16) as rt:
+            rt.device_run(events[:c.window])
+            mean, per = rt.device_run(events[c.window:])
+        p50 = nearest_rank(per, 0.5)
+        step_bytes = weight_bytes_per_step(c, 2) + b * kv_bytes_per_step(c, 4, c.window)
+        gbs = step_bytes / (mean * 1e-6) / 1e9
+        out[f'B{b}'] = {'p50_us_per_step': round(p50, 2), 'mean_us_per_step': round(mean, 2),
+                        'events_per_s': round(b / (p50 * 1e-6)), 'algorithmic_bytes_per_step': step_bytes,
+                        'achieved_gbs': round(gbs, 1), 'hbm_frac': round(gbs / HBM_PEAK_GBS, 4)}
+    return out
 
 
 def nearest_rank(values, q):
@@ -115,9 +142,14 @@ def main():
     ap.add_argument('--backend', choices=['fused', 'graph', 'cuda'], default='fused')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--quick', action='store_true', help='skip the secondary measurements')
+    ap.add_argument('--batched', action='store_true',
+                    help='only the batched-streams measurement (B in 1, 16, 64, 256; --steps timed steps each)')
     ap.add_argument('--copy-calibration', type=int, metavar='MIB', default=0,
                     help='only run 8 plain device copies of MIB MiB (reference kernel for HBM counters)')
     args = ap.parse_args()
+    if args.batched:
+        print(json.dumps(batched_streams(steps=args.steps)), flush=True)
+        return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return
@@ -177,6 +209,9 @@ def main():
                 host.append((time.perf_counter() - s) * 1e6)
             extra['persistent_service_p50_us'] = nearest_rank(host, 0.5)
             extra['persistent_service_p99_us'] = nearest_rank(host, 0.99)
+
+    if not args.quick:
+        extra['batched'] = batched_streams()
 
     achieved = bytes_step / (mean_us * 1e-6) / 1e9
     roofline = {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
