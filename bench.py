@@ -13,8 +13,9 @@ already resident in HBM). The library synchronizes its stream before and after t
 launches. One JSON line is printed.
 
 Secondary measurements (skipped with --quick) go under "extra": host-service latency through
-step(), the device loop, the persistent worker, and B independent streams over shared weights
-(Main, bfloat16 weights, W=128, B in 1, 16, 64, 256; --batched runs only that).
+step(), the device loop, the persistent worker, B independent streams over shared weights
+(Main, bfloat16 weights, W=128, B in 1, 16, 64, 256; --batched runs only that), and the Main
+window sweep (W in 32..512, bfloat16 weights and mixed mode).
 
 Usage: python bench.py [--gpus 1] [--steps 1024] [--warmup 64] [--config large|main|small]
                        [--precision fp32|bf16w|mixed] [--no-cpu-baseline] [--quick] [--batched]
@@ -78,6 +79,33 @@ def batched_streams(counts=(1, 16, 64, 256), steps=64):
         out[f'B{b}'] = {'p50_us_per_step': round(p50, 2), 'mean_us_per_step': round(mean, 2),
                         'events_per_s': round(b / (p50 * 1e-6)), 'algorithmic_bytes_per_step': step_bytes,
                         'achieved_gbs': round(gbs, 1), 'hbm_frac': round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def window_sweep(windows=(32, 64, 128, 256, 512), steps=2048):
+    """Main architecture, one stream, fused backend, W in `windows`: bfloat16 weights with FP32
+    K/V, and the reference's mixed mode (FP16 weights and K/V). Weights and inputs from seed 2.
+    Each W fills its window (untimed), then times `steps` full-window steps. Shows how the
+    attention's K/V bytes grow against the fixed weight bytes."""
+    base, _ = CONFIGS['main']
+    out = {'workload': 'main single-stream window sweep, fused backend', 'steps': steps}
+    for mode in ('bf16w', 'mixed'):
+        mixed = mode == 'mixed'
+        rows = {}
+        for w in windows:
+            c = ModelConfig(base.layers, base.width, base.heads, base.ffn, w, base.features)
+            weights = synthetic_checkpoint(c, seed=2, mixed=mixed)
+            events = np.random.default_rng([2, 1]).standard_normal((w - 1 + steps, c.features), dtype=np.float32)
+            opts = RuntimeOptions(backend=Backend.FUSED, blocks=0,
+                                  weight_dtype=WeightStorage.AS_MODEL if mixed else WeightStorage.BF16)
+            with Runtime((c, weights, mixed), opts) as rt:
+                rt.device_run(events[:w - 1], reset=True)
+                mean, per = rt.device_run(events[w - 1:])
+            step_bytes = weight_bytes_per_step(c, 2) + kv_bytes_per_step(c, 2 if mixed else 4, w)
+            gbs = step_bytes / (mean * 1e-6) / 1e9
+            rows[f'W{w}'] = {'p50_us': round(nearest_rank(per, 0.5), 2), 'p99_us': round(nearest_rank(per, 0.99), 2),
+                             'algorithmic_bytes_per_step': step_bytes, 'achieved_gbs': round(gbs, 1)}
+        out[mode] = rows
     return out
 
 
@@ -212,6 +240,7 @@ def main():
 
     if not args.quick:
         extra['batched'] = batched_streams()
+        extra['window_sweep'] = window_sweep()
 
     achieved = bytes_step / (mean_us * 1e-6) / 1e9
     roofline = {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',

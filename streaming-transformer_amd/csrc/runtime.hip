@@ -241,7 +241,7 @@ class Runtime {
   hipGraphExec_t graph_exec_ = nullptr;
   DeviceBuffer weights_, keys_, values_, scratch_, tagged_, position_, epoch_, rope_, args_dev_;
   PinnedBuffer host_in_, host_out_;
-  MappedBuffer mailbox_, mapped_in_;
+  MappedBuffer mailbox_, mapped_in_, mapped_snap_;
   uint64_t sequence_ = 0;
   hipStream_t copy_stream_ = nullptr;
   StepArgs args_{};
@@ -408,6 +408,10 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
     a.mb_checksum = &dmb->checksum;
     a.mb_error = &dmb->error;
     a.mapped_input = reinterpret_cast<const float*>(mapped_in_.dev);
+    const int kvb = prec_ == kMixed ? 2 : 4;
+    mapped_snap_.alloc(kSnapKeys + 2 * (size_t)snapshot_ring_bytes(c_.layers, c_.width, c_.window, kvb) +
+                       (size_t)c_.layers * c_.width * 4);
+    a.mapped_snapshot = reinterpret_cast<unsigned char*>(mapped_snap_.dev);
     a.idle_ticks = (unsigned long long)(options.idle_seconds * (double)wall_khz_ * 1000.0);
     a.max_events = options.max_events;
     a.initial_sequence = options.initial_sequence;
@@ -701,11 +705,32 @@ void Runtime::command(int cmd) {
   if (mb->error) throw Error(ST_ERR_NUMERIC, "Device watchdog tripped (error bits " + std::to_string(mb->error) + ")");
 }
 
-// Snapshot (src/cuda/Runtime.cu:548-568). Copies run on their own stream: with a persistent
-// worker the runtime's stream is occupied, and the worker's state writes are written through
-// to memory before it completes a command.
+// Snapshot (src/cuda/Runtime.cu:548-568). With a live persistent worker, the worker itself
+// copies the state into mapped host memory (a SNAPSHOT command): a device-to-host copy on
+// another queue would wait for the resident worker to end. Otherwise the state is copied
+// after the stream has drained.
 void Runtime::snapshot(uint64_t* position, float* keys, float* values, float* hidden) {
-  if (!persistent() || !running_) sync();
+  if (persistent() && running_ && !__atomic_load_n(&mailbox()->exited, __ATOMIC_ACQUIRE)) {
+    command(kCmdSnapshot);
+    const unsigned char* s = reinterpret_cast<const unsigned char*>(mapped_snap_.ptr);
+    const size_t n = (size_t)c_.layers * c_.width * c_.window;
+    const size_t ring = snapshot_ring_bytes(c_.layers, c_.width, c_.window, prec_ == kMixed ? 2 : 4);
+    if (position) std::memcpy(position, s, 8);
+    auto decode = [&](const unsigned char* src, float* dst) {
+      if (!dst) return;
+      if (prec_ == kMixed) {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(src);
+        for (size_t i = 0; i < n; i++) dst[i] = host_half_to_float(h[i]);
+      } else {
+        std::memcpy(dst, src, n * 4);
+      }
+    };
+    decode(s + kSnapKeys, keys);
+    decode(s + kSnapKeys + ring, values);
+    if (hidden) std::memcpy(hidden, s + kSnapKeys + 2 * ring, (size_t)c_.layers * c_.width * 4);
+    return;
+  }
+  sync();
   auto copy = [&](void* dst, const void* src, size_t bytes) {
     HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, copy_stream_));
     HIP_CHECK(hipStreamSynchronize(copy_stream_));

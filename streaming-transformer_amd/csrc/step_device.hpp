@@ -67,7 +67,7 @@ enum PhaseKind : int { kInput = 0, kQkv, kAttn, kOut, kGateUp, kDown, kFinal };
 enum ErrorBits : unsigned { kErrPollTimeout = 1u, kErrMailboxTimeout = 2u };
 // Mailbox commands (the reference's Command enum, src/cuda/Primitives.cuh:14), plus the
 // worker's own exit on an exhausted idle budget.
-enum MailboxCommand : int { kCmdRun = 1, kCmdReset = 2, kCmdStop = 3, kCmdPing = 4, kCmdExit = 64 };
+enum MailboxCommand : int { kCmdRun = 1, kCmdReset = 2, kCmdStop = 3, kCmdPing = 4, kCmdSnapshot = 5, kCmdExit = 64 };
 
 // Buffer-resource dword3 for raw buffer access on gfx9 (32-bit data format).
 constexpr int kRsrcWord3 = 0x00020000;
@@ -120,6 +120,7 @@ struct StepArgs {
   unsigned long long* mb_checksum;
   unsigned* mb_error;              // device error bits, copied out with each completion
   const float* mapped_input;       // the host's event buffer
+  unsigned char* mapped_snapshot;  // SNAPSHOT destination in host memory (layout: snapshot_owned)
   unsigned long long idle_ticks;   // idle budget before the worker exits
   unsigned long long max_events;   // RUN budget (0 = unlimited)
   unsigned long long initial_sequence;

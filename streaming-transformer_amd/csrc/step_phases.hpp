@@ -1392,8 +1392,48 @@ __device__ __forceinline__ void reset_owned(Ctx<P>& c) {
   if (c.g == 0 && threadIdx.x == 0) __hip_atomic_store(a.position, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// Byte offsets of the SNAPSHOT copy in host memory: position (8 bytes), then K and V as stored
+// in the ring, then the hidden state [L][d] FP32.
+constexpr uint32_t kSnapKeys = 256;
+__host__ __device__ __forceinline__ uint32_t snapshot_ring_bytes(int layers, int width, int window, int kv_bytes) {
+  return (uint32_t)layers * (uint32_t)width * (uint32_t)window * (uint32_t)kv_bytes;
+}
+
+// SNAPSHOT (persistent worker): copy the carried state into the host buffer while the worker
+// stays resident (copy commands on another queue cannot start while the worker holds every
+// CU). Each workgroup copies the ring chunks of the RESET split and a grid-strided share of the
+// hidden state, all with coherent loads; workgroup 0 writes the position. The stores go to
+// fine-grained host memory; the worker releases them (system scope) before reporting done.
+template <int P>
+__device__ __forceinline__ void snapshot_owned(Ctx<P>& c, unsigned long long t) {
+  const StepArgs& a = c.a;
+  unsigned char* out = a.mapped_snapshot;
+  const uint32_t ring = snapshot_ring_bytes(a.layers, a.width, a.window, Traits<P>::kKvBytes);
+  const int nch = (a.window + a.chunk - 1) / a.chunk;
+  const int total = a.heads * nch;
+  for (int it = c.g; it < total; it += c.grid) {
+    const int h = it / nch, ch = it - h * nch;
+    const int row0 = ch * a.chunk;
+    const int rows = a.window - row0 < a.chunk ? a.window - row0 : a.chunk;
+    const uint32_t bytes = (uint32_t)rows * (uint32_t)a.dim * Traits<P>::kKvBytes;  // a multiple of 4
+    for (int l = 0; l < a.layers; l++) {
+      const uint32_t b0 = ((uint32_t)(l * a.heads + h) * (uint32_t)a.window + (uint32_t)row0) * (uint32_t)a.dim *
+                          Traits<P>::kKvBytes;
+      for (uint32_t off = threadIdx.x * 4u; off < bytes; off += kThreads * 4u) {
+        *reinterpret_cast<float*>(out + kSnapKeys + b0 + off) = ld4_coherent(c.kr, b0 + off);
+        *reinterpret_cast<float*>(out + kSnapKeys + ring + b0 + off) = ld4_coherent(c.vr, b0 + off);
+      }
+    }
+  }
+  float* hidden = reinterpret_cast<float*>(out + kSnapKeys + 2u * ring);
+  for (int i = c.g * kThreads + (int)threadIdx.x; i < a.layers * a.width; i += c.grid * kThreads)
+    hidden[i] = ld4_coherent(c.sr, (a.s_hidden + (uint32_t)i) * 4u);
+  if (c.g == 0 && threadIdx.x == 0) *reinterpret_cast<unsigned long long*>(out) = t;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+}
+
 // Persistent worker (Backend::PERSISTENT): one cooperative launch serves RUN / RESET / PING /
-// STOP commands from a host mailbox, following the reference's persistent_kernel
+// SNAPSHOT / STOP commands from a host mailbox, following the reference's persistent_kernel
 // (src/cuda/Runtime.cu:58-122) and its ordering contract (docs/transport.md:9-16):
 //  - workgroup 0's control wave acquires the request word (system scope), stages a RUN's
 //    event into the tagged vector t_in and publishes the command as the tagged word t_cmd
@@ -1466,6 +1506,8 @@ __global__ __launch_bounds__(kThreads) void persistent_kernel(const StepArgs* __
     } else if (cmd == kCmdReset) {
       reset_owned(c);
       t = 0;
+    } else if (cmd == kCmdSnapshot) {
+      snapshot_owned(c, t);
     } else if (cmd == kCmdPing && c.g == 0 && threadIdx.x == 0) {
       unsigned long long sum = 0;
       for (int i = 0; i < a.features; i++) sum += __builtin_bit_cast(unsigned, a.mapped_input[i]);

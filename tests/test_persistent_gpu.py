@@ -114,6 +114,34 @@ def test_fixture_trace_equals_fused_bit_for_bit(golden, blocks):
         np.testing.assert_array_equal(a, b)
 
 
+@pytest.mark.parametrize('mode', ['fp32', 'mixed'])
+def test_snapshots_while_worker_runs(golden, mode):
+    # The reference's validation snapshots a live persistent runtime between commands
+    # (scripts/validate.py:55-74). The worker serves each snapshot and keeps running: every
+    # snapshot equals the fused backend's at the same event, and returns promptly (a copy
+    # that waited for the worker would only return after the idle budget).
+    g = golden(f'small-{mode}')
+    points = {5, 17, 40, 63, 64, 90}
+    states = []
+    for make in (lambda: persistent(g.checkpoint, 0),
+                 lambda: Runtime(g.checkpoint, RuntimeOptions(backend=Backend.FUSED, blocks=0))):
+        got = []
+        with make() as rt:
+            for i, e in enumerate(g.trace[:100]):
+                if i == 70:
+                    rt.reset()
+                rt.step(e)
+                if i in points:
+                    t0 = time.perf_counter()
+                    got.append(rt.snapshot())
+                    assert time.perf_counter() - t0 < 2.0
+        states.append(got)
+    for a, b in zip(*states):
+        assert a[0] == b[0]
+        for x, y in zip(a[1:], b[1:]):
+            np.testing.assert_array_equal(x, y)
+
+
 def test_main_shape_matches_oracle():
     c = ModelConfig(8, 512, 8, 2048, 128, 512)
     w = synthetic_checkpoint(c, seed=7)
