@@ -13,7 +13,8 @@ already resident in HBM). The library synchronizes its stream before and after t
 launches. One JSON line is printed.
 
 Secondary measurements (skipped with --quick) go under "extra": host-service latency through
-step(), the device loop, the persistent worker, B independent streams over shared weights
+step(), the device loop, the persistent worker, the vendor GEMV baseline (rocBLAS projections
+in a captured graph) on the same workload, B independent streams over shared weights
 (Main, bfloat16 weights, W=128, B in 1, 16, 64, 256; --batched runs only that), and the Main
 window sweep (W in 32..512, bfloat16 weights and mixed mode).
 
@@ -238,6 +239,13 @@ def main():
             extra['persistent_service_p50_us'] = nearest_rank(host, 0.5)
             extra['persistent_service_p99_us'] = nearest_rank(host, 0.99)
 
+    if not args.quick and args.precision != 'bf16w':
+        # The same workload through the vendor GEMV baseline (rocBLAS projections, captured).
+        vopts = RuntimeOptions(backend=Backend.CUBLAS_GRAPH, blocks=0)
+        with Runtime((c, weights, mixed), vopts) as rt:
+            rt.device_run(events[:fill], reset=True)
+            _, vper = rt.device_run(events[fill:fill + min(args.steps, 256)])
+        extra['vendor_gemv_graph_p50_us'] = nearest_rank(vper, 0.5)
     if not args.quick:
         extra['batched'] = batched_streams()
         extra['window_sweep'] = window_sweep()

@@ -32,8 +32,10 @@ enum {
 
 /* Stream::Backend (include/Runtime.hpp:7). CUDA = staged HIP kernels, GRAPH = the staged
  * sequence captured in a hipGraph, FUSED = one cooperative launch per step, PERSISTENT =
- * resident kernel driven through a host mailbox. CUBLAS / CUBLAS_GRAPH (vendor GEMV
- * baselines) are not provided and are rejected with ST_ERR_INVALID. */
+ * resident kernel driven through a host mailbox. CUBLAS / CUBLAS_GRAPH are the vendor GEMV
+ * baselines (src/cuda/Runtime.cu:330-385): the projections run in rocBLAS (sgemv for FP32,
+ * gemm_ex FP16 -> FP32 for mixed), eagerly or captured in a hipGraph; they take the
+ * checkpoint's own weight storage (ST_WEIGHTS_BF16 is rejected). */
 enum {
   ST_BACKEND_CUDA = 0,
   ST_BACKEND_GRAPH = 1,

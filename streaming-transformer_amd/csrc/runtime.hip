@@ -8,6 +8,7 @@
 #include "../../include/st_runtime.h"
 
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <atomic>
@@ -184,6 +185,8 @@ static std::string probe_json() {
 
 // ---------------------------------------------------------------------------------------------
 
+#include "vendor_path.hpp"
+
 class Runtime {
  public:
   Runtime(const st_config& config, bool mixed, const st_tensor* tensors, size_t count,
@@ -226,6 +229,7 @@ class Runtime {
   void check_device_error();
   void sync() { HIP_CHECK(hipStreamSynchronize(stream_)); }
   bool persistent() const { return opt_.backend == ST_BACKEND_PERSISTENT; }
+  bool vendor() const { return opt_.backend == ST_BACKEND_CUBLAS || opt_.backend == ST_BACKEND_CUBLAS_GRAPH; }
   void reset_device();
   void start_worker();
   void command(int cmd);
@@ -247,6 +251,7 @@ class Runtime {
   StepArgs args_{};
   const StepArgs* dargs_ = nullptr;
   std::string probe_;
+  std::unique_ptr<VendorPath> vendor_;  // CUBLAS / CUBLAS_GRAPH
 };
 
 Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, size_t count,
@@ -257,8 +262,9 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
     throw Error(ST_ERR_INVALID, "Invalid blocks or idle budget");
   if (options.initial_sequence >= std::numeric_limits<uint64_t>::max() - 1)
     throw Error(ST_ERR_INVALID, "Initial sequence must leave room for RUN and STOP");
-  if (options.backend == ST_BACKEND_CUBLAS || options.backend == ST_BACKEND_CUBLAS_GRAPH)
-    throw Error(ST_ERR_INVALID, "Vendor-library backends are not provided by this build");
+  if ((options.backend == ST_BACKEND_CUBLAS || options.backend == ST_BACKEND_CUBLAS_GRAPH) &&
+      options.weight_dtype == ST_WEIGHTS_BF16)
+    throw Error(ST_ERR_INVALID, "Vendor GEMV backends take the checkpoint's own weight storage (FP32 or mixed)");
   if (options.backend < 0 || options.backend > ST_BACKEND_PERSISTENT)
     throw Error(ST_ERR_INVALID, "Unknown backend");
   if (options.weight_dtype == ST_WEIGHTS_BF16 && mixed)
@@ -422,6 +428,19 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   dargs_ = reinterpret_cast<const StepArgs*>(args_dev_.ptr);
 
   reset_device();
+  if (vendor()) {
+    vendor_ = std::make_unique<VendorPath>(c_, prec_ == kMixed, args_, tensors, count, stream_);
+    if (options.backend == ST_BACKEND_CUBLAS_GRAPH) {
+      // Warm the library outside capture, restore the initial state, then capture.
+      vendor_->launch();
+      sync();
+      reset_device();
+      HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+      vendor_->launch();
+      HIP_CHECK(hipStreamEndCapture(stream_, &graph_));
+      HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+    }
+  }
   if (options.backend == ST_BACKEND_GRAPH) {
     // Warm up outside capture, restore the initial state, then capture the phase sequence.
     launch_phases();
@@ -442,6 +461,7 @@ Runtime::~Runtime() {
   } catch (...) {
   }
   if (stream_) (void)hipStreamSynchronize(stream_);
+  vendor_.reset();  // the rocBLAS handle refers to the stream
   if (copy_stream_) (void)hipStreamDestroy(copy_stream_);
   if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
   if (graph_) (void)hipGraphDestroy(graph_);
@@ -598,8 +618,10 @@ void Runtime::launch_fused(const float* event) {
 }
 
 void Runtime::launch_step() {
-  if (opt_.backend == ST_BACKEND_GRAPH) HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
+  if (opt_.backend == ST_BACKEND_GRAPH || opt_.backend == ST_BACKEND_CUBLAS_GRAPH)
+    HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
   else if (opt_.backend == ST_BACKEND_FUSED) launch_fused();
+  else if (opt_.backend == ST_BACKEND_CUBLAS) vendor_->launch();
   else launch_phases();
 }
 

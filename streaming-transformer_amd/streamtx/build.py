@@ -16,6 +16,8 @@ HIPCC_FLAGS = [
     '-O3', '--offload-arch=gfx950', '-std=c++17', '-fPIC', '-shared', '-fno-strict-aliasing',
     # keep packed-FP32 VALU instructions out of the generated code
     '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+    # rocBLAS for the vendor GEMV backends
+    '-L/opt/rocm/lib', '-lrocblas', '-Wl,-rpath,/opt/rocm/lib',
 ]
 
 

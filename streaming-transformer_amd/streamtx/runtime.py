@@ -27,8 +27,8 @@ class Backend(enum.IntEnum):
     """Stream::Backend (include/Runtime.hpp:7)."""
     CUDA = 0          # staged HIP phase kernels
     GRAPH = 1         # staged sequence captured in a hipGraph
-    CUBLAS = 2        # not provided
-    CUBLAS_GRAPH = 3  # not provided
+    CUBLAS = 2        # vendor GEMV baseline: rocBLAS projections, HIP kernels for the rest
+    CUBLAS_GRAPH = 3  # the same captured in a hipGraph
     FUSED = 4         # one cooperative launch per step
     PERSISTENT = 5    # resident kernel + host mailbox
 

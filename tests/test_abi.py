@@ -10,7 +10,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from streamtx import Backend, ModelConfig, Runtime, RuntimeOptions, library, synthetic_checkpoint
+from streamtx import Backend, ModelConfig, Runtime, RuntimeOptions, WeightStorage, library, synthetic_checkpoint
 from streamtx.runtime import LIBRARY_PATH, _Options
 
 ROOT = Path(__file__).resolve().parent.parent
@@ -58,7 +58,7 @@ def test_invalid_config_rejected(field, value):
     (dict(idle_seconds=0), 'idle budget'),
     (dict(blocks=-1), 'idle budget'),
     (dict(initial_sequence=2**64 - 2), 'Initial sequence'),
-    (dict(backend=Backend.CUBLAS), 'not provided'),
+    (dict(backend=Backend.CUBLAS, weight_dtype=WeightStorage.BF16), 'own weight storage'),
 ])
 def test_invalid_options_rejected(opts, msg):
     c = ModelConfig(1, 64, 4, 128, 64, 32)

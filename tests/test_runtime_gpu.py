@@ -17,6 +17,8 @@ pytestmark = pytest.mark.gpu
 
 STRICT = dict(atol=1e-6, rtol=1e-5)
 BACKENDS = [(Backend.CUDA, 0), (Backend.GRAPH, 0), (Backend.FUSED, 1), (Backend.FUSED, 4), (Backend.FUSED, 0)]
+# Vendor GEMV baselines (rocBLAS projections): same parity bars, their own summation order.
+VENDOR = [(Backend.CUBLAS, 0), (Backend.CUBLAS_GRAPH, 0)]
 
 
 def runtime(model, backend, blocks, **kw):
@@ -24,7 +26,7 @@ def runtime(model, backend, blocks, **kw):
     return Runtime(model, RuntimeOptions(backend=backend, blocks=blocks, **kw))
 
 
-@pytest.mark.parametrize('backend,blocks', BACKENDS)
+@pytest.mark.parametrize('backend,blocks', BACKENDS + VENDOR)
 def test_fp32_fixture_every_event(golden, backend, blocks):
     g = golden('small-fp32')
     oracle = Oracle(g.config, g.checkpoint.tensors, accumulate='double')
@@ -45,7 +47,8 @@ def test_fp32_fixture_every_event(golden, backend, blocks):
                 assert numerical.fp32_strict_failures(a, o, **STRICT) == 0, (i, float(np.abs(a - o).max()))
 
 
-@pytest.mark.parametrize('backend,blocks', [(Backend.CUDA, 0), (Backend.GRAPH, 0), (Backend.FUSED, 0)])
+@pytest.mark.parametrize('backend,blocks', [(Backend.CUDA, 0), (Backend.GRAPH, 0), (Backend.FUSED, 0),
+                                            (Backend.CUBLAS, 0), (Backend.CUBLAS_GRAPH, 0)])
 def test_mixed_fixture_policy_v3(golden, backend, blocks):
     g = golden('small-mixed')
     scores, refs = [], []
@@ -209,3 +212,34 @@ def test_stopped_runtime_rejects_commands():
             rt.step(np.ones(c.features, np.float32))
         with pytest.raises(RuntimeError, match='stopped'):
             rt.reset()
+
+
+@pytest.mark.parametrize('name,steps,reset_at', [('main', 140, 131), ('dh48', 60, 41)])
+def test_vendor_backends_match_oracle_and_graph_replays_match_eager(name, steps, reset_at):
+    # The rocBLAS baseline against the oracle at the FP32 bar, and its captured graph against
+    # eager launches bit for bit (graph replays interleaved with the host's own work).
+    c = SHAPES[name]
+    w = synthetic_checkpoint(c, seed=9)
+    events = _stream(c, 9, steps)
+    oracle = Oracle(c, w, accumulate='double', threads=8)
+    results = []
+    for backend in (Backend.CUBLAS, Backend.CUBLAS_GRAPH):
+        scores = []
+        with runtime((c, w, False), backend, 0) as rt:
+            for i, e in enumerate(events):
+                if i == reset_at:
+                    rt.reset()
+                    if backend == Backend.CUBLAS:
+                        oracle.reset()
+                got = rt.step(e)
+                scores.append(got)
+                if backend == Backend.CUBLAS:
+                    ref = oracle.step(e)
+                    assert numerical.fp32_strict_failures([got], [ref], **STRICT) == 0, (i, got, ref)
+            results.append((np.array(scores, dtype=np.float32), rt.snapshot()))
+    (s0, st0), (s1, st1) = results
+    np.testing.assert_array_equal(s0, s1)
+    _, ok, ov, oh = oracle.snapshot()
+    for a, b, o in zip(st0[1:], st1[1:], (ok, ov, oh)):
+        np.testing.assert_array_equal(a, b)
+        assert numerical.fp32_strict_failures(a, o, **STRICT) == 0, float(np.abs(a - o).max())
