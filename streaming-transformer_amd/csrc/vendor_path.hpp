@@ -26,6 +26,7 @@ struct VendorArgs {
   float* y;                       // [max(3d, 2F)] GEMV output
   float* q;                       // [d] rotated query
   float* score;                   // [1] score GEMV output
+  float* part;                    // attention partials [H][chunks][dh + 2]: o, max, exp sum
 };
 
 constexpr int kVendorThreads = 256;
@@ -115,44 +116,125 @@ __device__ __forceinline__ float ring_at(const void* ring, size_t i) {
   return reinterpret_cast<const float*>(ring)[i];
 }
 
-// Attention of one head over the valid window (src/cuda/Primitives.cuh:167-219): logits
-// q.K/sqrt(dh), softmax, weighted V, cast; FP16 copy of the output for the mixed GEMM.
-// Dynamic LDS holds `window` probabilities.
+// Attention (src/cuda/Primitives.cuh:167-219) in two kernels, so that the window is read by
+// many workgroups: vnd_attn_part computes, for one (head, 64-slot chunk), the chunk's logit
+// maximum m, exp sum s and unnormalized output o = sum_j e^(l_j - m) V_j; vnd_attn_combine
+// merges a head's chunks in chunk order: out = sum_c o_c e^(m_c - M) / sum_c s_c e^(m_c - M),
+// then casts. Chunks past the valid window report m = -inf, s = 0.
+// vnd_attn_part: 256 threads = 16 groups of 16 lanes. Logits: a group per K row (lane r
+// covers elements 4r .. 4r+3 of each 64-element piece), a 16-lane DPP sum. Values: group g
+// sums its slots' V rows, the 16 groups summed in LDS in group order.
+constexpr int kAttnChunk = 64;
+constexpr int kAttnPartThreads = 256;
 template <bool M>
-__global__ __launch_bounds__(kVendorThreads) void vnd_attention(const VendorArgs* __restrict__ ap, int layer) {
+__global__ __launch_bounds__(kAttnPartThreads) void vnd_attn_part(const VendorArgs* __restrict__ ap, int layer) {
   const VendorArgs& a = *ap;
-  extern __shared__ float pr[];
-  __shared__ float red[kVendorThreads / 64];
-  const int h = blockIdx.x, dim = a.dim;
+  __shared__ float pr[kAttnChunk];
+  __shared__ float red[kAttnPartThreads / 64];
+  __shared__ float4 vred[16][17];
+  const int nch = (a.window + kAttnChunk - 1) / kAttnChunk;
+  const int h = blockIdx.x / nch, ch = blockIdx.x - h * nch;
+  const int dim = a.dim, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = tid & 15, grp = tid >> 4;
   const unsigned long long t = *a.position;
   const int valid = t + 1 < (unsigned long long)a.window ? (int)(t + 1) : a.window;
+  const int s0 = ch * kAttnChunk, s1 = min(valid, s0 + kAttnChunk);
+  float* part = a.part + (size_t)blockIdx.x * (dim + 2);
+  if (s0 >= valid) {  // uniform over the workgroup
+    for (int d = tid; d < dim; d += blockDim.x) part[d] = 0.f;
+    if (tid == 0) {
+      part[dim] = -INFINITY;
+      part[dim + 1] = 0.f;
+    }
+    return;
+  }
   const size_t base = ((size_t)layer * a.heads + h) * (size_t)a.window * dim;
   const float* q = a.q + h * dim;
   const float div = sqrtf((float)dim);
   float mx = -INFINITY;
-  for (int s = threadIdx.x; s < valid; s += blockDim.x) {
+  for (int sb = s0; sb < s1; sb += 16) {
+    const int s = sb + grp;
+    const size_t row = base + (size_t)(s < s1 ? s : s1 - 1) * dim;
     float dot = 0.f;
-    for (int d = 0; d < dim; d++) dot += q[d] * ring_at<M>(a.keys, base + (size_t)s * dim + d);
-    const float lg = dot / div;
-    pr[s] = lg;
-    mx = fmaxf(mx, lg);
+    for (int d = 4 * r; d < dim; d += 64)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        if (d + j < dim) dot += q[d + j] * ring_at<M>(a.keys, row + d + j);
+    dot = group_sum(dot, 16);
+    if (s < s1) {
+      const float lg = dot / div;
+      if (r == 0) pr[s - s0] = lg;
+      mx = fmaxf(mx, lg);
+    }
   }
   mx = wave_top(mx);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  if (lane == 0) red[wave] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   __syncthreads();
   float sum = 0.f;
-  for (int s = threadIdx.x; s < valid; s += blockDim.x) {
-    const float e = expf(pr[s] - mx);
-    pr[s] = e;
-    sum += e;
+  if (tid < s1 - s0) {
+    const float e = expf(pr[tid] - mx);
+    pr[tid] = e;
+    sum = e;
   }
-  sum = block_sum(sum, red);
+  sum = wave_total(sum);
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  sum = (red[0] + red[1]) + (red[2] + red[3]);
+  for (int d0 = 0; d0 < dim; d0 += 64) {
+    const int d = d0 + 4 * r;
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s = s0 + grp; s < s1; s += 16) {
+      const float p = pr[s - s0];
+      const size_t row = base + (size_t)s * dim;
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        if (d + j < dim) o[j] += p * ring_at<M>(a.values, row + d + j);
+    }
+    vred[grp][r] = make_float4(o[0], o[1], o[2], o[3]);
+    __syncthreads();
+    if (tid < 16) {
+      float4 acc = vred[0][tid];
+      for (int k = 1; k < 16; k++) {
+        const float4 v = vred[k][tid];
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+      }
+      const float vals[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        if (d0 + 4 * tid + j < dim) part[d0 + 4 * tid + j] = vals[j];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    part[dim] = mx;
+    part[dim + 1] = sum;
+  }
+}
+
+template <bool M>
+__global__ __launch_bounds__(64) void vnd_attn_combine(const VendorArgs* __restrict__ ap) {
+  const VendorArgs& a = *ap;
+  const int nch = (a.window + kAttnChunk - 1) / kAttnChunk;
+  const int h = blockIdx.x, dim = a.dim;
+  const float* part = a.part + (size_t)h * nch * (dim + 2);
+  float mx = -INFINITY;
+  for (int c = 0; c < nch; c++) mx = fmaxf(mx, part[(size_t)c * (dim + 2) + dim]);
+  float total = 0.f;
+  for (int c = 0; c < nch; c++) {
+    const float* p = part + (size_t)c * (dim + 2);
+    total += p[dim + 1] * expf(p[dim] - mx);
+  }
   for (int d = threadIdx.x; d < dim; d += blockDim.x) {
     float o = 0.f;
-    for (int s = 0; s < valid; s++) o += pr[s] * ring_at<M>(a.values, base + (size_t)s * dim + d);
-    const float v = vcast<M>(o / sum);
+    for (int c = 0; c < nch; c++) {
+      const float* p = part + (size_t)c * (dim + 2);
+      o += p[d] * expf(p[dim] - mx);
+    }
+    const float v = vcast<M>(o / total);
     a.xn[h * dim + d] = v;
     if constexpr (M) a.xh[h * dim + d] = float_to_half(v);
   }
@@ -236,6 +318,7 @@ class VendorPath {
     a.y = alloc(y_, out);
     a.q = alloc(q_, c.width);
     a.score = alloc(score_, 1);
+    a.part = alloc(part_, (size_t)c.heads * ((c.window + kAttnChunk - 1) / kAttnChunk) * (c.width / c.heads + 2));
     // FP32 view of the input projection (the arena holds FP16 for a mixed model).
     const float* input = nullptr;
     for (size_t i = 0; i < count; i++)
@@ -279,6 +362,7 @@ class VendorPath {
   void launch_t() {
     const VendorArgs& a = args_;
     const int d = c_.width, F = c_.ffn, T = kVendorThreads;
+    const int chunks = (c_.window + kAttnChunk - 1) / kAttnChunk;
     const float one = 1.f, zero = 0.f;
     // Input projection on the FP32 weights and the FP32 event.
     ROCBLAS_CHECK(rocblas_sgemv(handle_, rocblas_operation_transpose, c_.features, d, &one,
@@ -290,7 +374,8 @@ class VendorPath {
       else hipLaunchKernelGGL((vnd_norm<M, false>), dim3(1), dim3(T), 0, stream_, dargs_, w.norm1);
       gemv(w.qkv, a.width_p, 3 * d, d, M, a.xn, a.y);
       hipLaunchKernelGGL((vnd_rope_ring<M>), dim3((3 * d / 2 + T - 1) / T), dim3(T), 0, stream_, dargs_, l);
-      hipLaunchKernelGGL((vnd_attention<M>), dim3(c_.heads), dim3(T), (size_t)c_.window * 4, stream_, dargs_, l);
+      hipLaunchKernelGGL((vnd_attn_part<M>), dim3(c_.heads * chunks), dim3(kAttnPartThreads), 0, stream_, dargs_, l);
+      hipLaunchKernelGGL((vnd_attn_combine<M>), dim3(c_.heads), dim3(64), 0, stream_, dargs_);
       gemv(w.out, a.width_p, d, d, M, a.xn, a.y);
       hipLaunchKernelGGL((vnd_residual<M>), dim3((d + T - 1) / T), dim3(T), 0, stream_, dargs_, l, 0);
       hipLaunchKernelGGL((vnd_norm<M, false>), dim3(1), dim3(T), 0, stream_, dargs_, w.norm2);
@@ -310,7 +395,7 @@ class VendorPath {
   const StepArgs& s_;
   hipStream_t stream_;
   rocblas_handle handle_ = nullptr;
-  DeviceBuffer workspace_, x_, xn_, xh_, y_, q_, score_, input_f32_, args_dev_;
+  DeviceBuffer workspace_, x_, xn_, xh_, y_, q_, score_, part_, input_f32_, args_dev_;
   VendorArgs args_{};
   const VendorArgs* dargs_ = nullptr;
 };
