@@ -39,175 +39,226 @@ struct BatchArgs {
   float* score;                    // [B]
 };
 
-constexpr int kProjWaves = 8;    // K-slices of a projection workgroup, one per wave
+constexpr int kSlices = 8;       // K-slices of a projection, K / 8 columns each
 constexpr int kGroupTiles = 4;   // most batch tiles (16 streams each) per projection workgroup
 
 enum BatchEpilogue : int { kEpInput = 0, kEpQkv, kEpOut, kEpGateUp, kEpDown };
 
-// One projection Y = X . W^T over the batch, with its phase's epilogue. Workgroup
-// (column tile of 16 outputs, group of NT batch tiles); each of its 8 waves takes one
-// K-slice of K / 8 columns and accumulates the group's tiles with v_mfma_f32_16x16x4_f32.
-// The slices are summed in LDS in wave order, so a stream's outputs depend only on its own
-// row (bit-identical for any batch size and grouping). The padded batch is a multiple of NT
-// tiles, so the loop has no branches and the compiler keeps several k blocks of loads in
-// flight.
-// MFMA 16x16x4 layout: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16]; register r
-// of lane l holds D[4 (l / 16) + r][l % 16]. The four MFMA steps of a 16-wide k block use
-// k = kb + 4 (l / 16) + c for step c, the same index for A and B.
+// The exact three-term bfloat16 split of FP32 values, x = hi + mid + lo: truncations, hi keeps
+// the top 8 significand bits, mid the next 8 of the remainder, lo the rest (at most 8 bits).
+// Each term times a bfloat16 weight is exact in an FP32 accumulator.
+__device__ __forceinline__ void split3(const float (&x)[8], unsigned (&ph)[4], unsigned (&pm)[4], unsigned (&pl)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    unsigned h2[2], m2[2], l2[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const float v = x[2 * i + j];
+      const unsigned hb = __builtin_bit_cast(unsigned, v) & 0xffff0000u;
+      const float r1 = v - __builtin_bit_cast(float, hb);
+      const unsigned mb = __builtin_bit_cast(unsigned, r1) & 0xffff0000u;
+      const float r2 = r1 - __builtin_bit_cast(float, mb);
+      h2[j] = hb;
+      m2[j] = mb;
+      l2[j] = __builtin_bit_cast(unsigned, r2) & 0xffff0000u;
+    }
+    ph[i] = h2[1] | (h2[0] >> 16);
+    pm[i] = m2[1] | (m2[0] >> 16);
+    pl[i] = l2[1] | (l2[0] >> 16);
+  }
+}
+
+// One projection Y = X . W^T over the batch, with its phase's epilogue. Workgroup: CT column
+// tiles of 16 outputs and NT batch tiles of 16 streams. K is cut into 8 slices; each wave
+// accumulates SW of them (8 / SW waves) for every tile pair with MFMA, reusing each X
+// fragment for the CT column tiles and each weight fragment for the NT batch tiles. The slice
+// partials are added in one fixed pairwise tree, ((s0 + s1) + (s2 + s3)) + ((s4 + s5) +
+// (s6 + s7)), whatever NT, CT and SW are, so a stream's outputs depend only on its own row
+// and are bit-identical for every batch size. The padded batch is a multiple of NT tiles, so
+// the loops have no branches.
+// FP32 weights: v_mfma_f32_16x16x4_f32, k block of 16; lane l supplies A[l % 16][l / 16] and
+// B[l / 16][l % 16], register r of lane l holds D[4 (l / 16) + r][l % 16]; the four MFMA
+// steps use k = kb + 4 (l / 16) + c for step c, the same index for A and B.
+// bfloat16 weights: v_mfma_f32_16x16x32_bf16, k block of 32, on the exact split of the FP32
+// activation (3 MFMAs), so the product is the FP32 path's up to accumulation order. Lane
+// (r16, g) holds k = kb + 8 g .. + 7 for both operands; the sum over k does not depend on how
+// the hardware orders the lane groups.
 // kNorm: X is the residual stream x and the projection consumes RMSNorm(x) . g
 // (src/cuda/Primitives.cuh:122-135). The waves feed x * g to the MFMAs, accumulate the row's
 // sum of squares from the same loads, and the epilogue scales the row by
 // 1 / sqrt(sum / d + eps).
-template <int P, int E, bool kNorm, int NT>
-__global__ __launch_bounds__(512) void batch_proj(const BatchArgs* __restrict__ ap, const float* __restrict__ X, int ldx,
-                                                  uint32_t woff, int ldw, int N, int K, uint32_t w_norm, int layer) {
+template <int P, int E, bool kNorm, int NT, int CT, int SW>
+__global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs* __restrict__ ap,
+                                                               const float* __restrict__ X, int ldx, uint32_t woff,
+                                                               int ldw, int N, int K, uint32_t w_norm, int layer) {
+  constexpr int kWaves = kSlices / SW;
   const BatchArgs& a = *ap;
-  __shared__ float red[kProjWaves][NT][16][17];
-  __shared__ float sq[kProjWaves][NT][16];
+  __shared__ float red[kWaves][NT][CT][16][17];
+  __shared__ float sq[kWaves][NT][16];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int n0 = blockIdx.x * kBatchTile;
+  const int n0 = blockIdx.x * kBatchTile * CT;
   const int t0 = blockIdx.y * NT;
   const int r16 = lane & 15, g = lane >> 4;
-  const int slice = K / kProjWaves;
-  const int k0 = wave * slice, k1 = k0 + slice;
-  f4v acc[NT];
-  float ss[NT];
+  const int slice = K / kSlices;
+  f4v acc[SW][NT][CT];
+  float ss[SW][NT];
 #pragma unroll
-  for (int t = 0; t < NT; t++) {
-    acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
-    ss[t] = 0.f;
-  }
+  for (int i = 0; i < SW; i++)
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      ss[i][t] = 0.f;
+#pragma unroll
+      for (int c = 0; c < CT; c++) acc[i][t][c] = f4v{0.f, 0.f, 0.f, 0.f};
+    }
   if constexpr (P == kFp32) {
-    // k block of 16: four v_mfma_f32_16x16x4_f32; lane (r16, g) holds k = kb + 4 g .. + 3.
     const float* xr = X + (size_t)(t0 * kBatchTile + r16) * ldx + 4 * g;
     const float* wr = reinterpret_cast<const float*>(a.weights + woff) + (size_t)(n0 + r16) * ldw + 4 * g;
     const float* gr = reinterpret_cast<const float*>(a.weights + w_norm) + 4 * g;
-    auto load = [&](int kb, float4& w, float4& gn, float4* xv) {
-      w = *reinterpret_cast<const float4*>(wr + kb);
-      // The norm vector holds `width` values (a multiple of 16): a group of 4 is all in or out.
-      gn = make_float4(0.f, 0.f, 0.f, 0.f);
-      if constexpr (kNorm)
-        if (kb + 4 * g < a.width) gn = *reinterpret_cast<const float4*>(gr + kb);
-#pragma unroll
-      for (int t = 0; t < NT; t++) xv[t] = *reinterpret_cast<const float4*>(xr + (size_t)t * kBatchTile * ldx + kb);
+    struct Frag {
+      float4 w[CT], gn, x[NT];
     };
-    float4 w, gn, xv[NT];
-    load(k0, w, gn, xv);
-    for (int kb = k0; kb < k1; kb += 16) {
-      // Issue the next block's loads before this block's MFMAs (the last block reloads itself).
-      float4 w2, gn2, xv2[NT];
-      load(kb + 16 < k1 ? kb + 16 : kb, w2, gn2, xv2);
+    auto load = [&](int k, Frag& f) {
+#pragma unroll
+      for (int c = 0; c < CT; c++) f.w[c] = *reinterpret_cast<const float4*>(wr + (size_t)c * kBatchTile * ldw + k);
+      // The norm vector holds `width` values (a multiple of 16): a group of 4 is all in or out.
+      f.gn = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (kNorm)
+        if (k + 4 * g < a.width) f.gn = *reinterpret_cast<const float4*>(gr + k);
+#pragma unroll
+      for (int t = 0; t < NT; t++) f.x[t] = *reinterpret_cast<const float4*>(xr + (size_t)t * kBatchTile * ldx + k);
+    };
+    auto mma = [&](int i, const Frag& f) {
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        float4 x = xv[t];
+        float4 x = f.x[t];
         if constexpr (kNorm) {
-          ss[t] += x.x * x.x;
-          ss[t] += x.y * x.y;
-          ss[t] += x.z * x.z;
-          ss[t] += x.w * x.w;
-          x.x *= gn.x;
-          x.y *= gn.y;
-          x.z *= gn.z;
-          x.w *= gn.w;
+          ss[i][t] += x.x * x.x;
+          ss[i][t] += x.y * x.y;
+          ss[i][t] += x.z * x.z;
+          ss[i][t] += x.w * x.w;
+          x.x *= f.gn.x;
+          x.y *= f.gn.y;
+          x.z *= f.gn.z;
+          x.w *= f.gn.w;
         }
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, w.x, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, w.y, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, w.z, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, w.w, acc[t], 0, 0, 0);
-      }
-      w = w2;
-      gn = gn2;
 #pragma unroll
-      for (int t = 0; t < NT; t++) xv[t] = xv2[t];
+        for (int c = 0; c < CT; c++) {
+          f4v& d = acc[i][t][c];
+          d = __builtin_amdgcn_mfma_f32_16x16x4f32(x.x, f.w[c].x, d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x4f32(x.y, f.w[c].y, d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x4f32(x.z, f.w[c].z, d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x4f32(x.w, f.w[c].w, d, 0, 0, 0);
+        }
+      }
+    };
+    if constexpr (SW == 1) {
+      // Issue the next block's loads before this block's MFMAs (the last block reloads itself).
+      const int k0 = wave * slice;
+      Frag cur;
+      load(k0, cur);
+      for (int kk = 0; kk < slice; kk += 16) {
+        Frag nxt;
+        load(k0 + (kk + 16 < slice ? kk + 16 : kk), nxt);
+        mma(0, cur);
+        cur = nxt;
+      }
+    } else {
+      for (int kk = 0; kk < slice; kk += 16) {
+        Frag f[SW];
+#pragma unroll
+        for (int i = 0; i < SW; i++) load((wave * SW + i) * slice + kk, f[i]);
+#pragma unroll
+        for (int i = 0; i < SW; i++) mma(i, f[i]);
+      }
     }
   } else {
-    // bfloat16 weights: k block of 32 on v_mfma_f32_16x16x32_bf16. The FP32 activation is
-    // split exactly into three bfloat16 terms, x = hi + mid + lo (truncations: hi keeps the
-    // top 8 significand bits, mid the next 8 of the remainder, lo the rest, at most 8 bits),
-    // and each term times the bfloat16 weight is exact in the FP32 accumulator, so the
-    // product is the FP32 path's up to accumulation order. Lane (r16, g) holds
-    // k = kb + 8 g .. + 7 for both operands; the sum over k does not depend on how the
-    // hardware orders the lane groups.
     const float* xr = X + (size_t)(t0 * kBatchTile + r16) * ldx + 8 * g;
     const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.weights + woff) + (size_t)(n0 + r16) * ldw + 8 * g;
     const uint16_t* gr = reinterpret_cast<const uint16_t*>(a.weights + w_norm) + 8 * g;
-    struct X8 {
-      float4 lo, hi;
+    struct Frag {
+      uint4 w[CT], gn;
+      float4 xlo[NT], xhi[NT];
     };
-    auto load = [&](int kb, uint4& w, uint4& gn, X8* xv) {
-      w = *reinterpret_cast<const uint4*>(wr + kb);
-      gn = make_uint4(0u, 0u, 0u, 0u);
+    auto load = [&](int k, Frag& f) {
+#pragma unroll
+      for (int c = 0; c < CT; c++) f.w[c] = *reinterpret_cast<const uint4*>(wr + (size_t)c * kBatchTile * ldw + k);
+      f.gn = make_uint4(0u, 0u, 0u, 0u);
       if constexpr (kNorm)
-        if (kb + 8 * g < a.width) gn = *reinterpret_cast<const uint4*>(gr + kb);
+        if (k + 8 * g < a.width) f.gn = *reinterpret_cast<const uint4*>(gr + k);
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        const float* p = xr + (size_t)t * kBatchTile * ldx + kb;
-        xv[t].lo = *reinterpret_cast<const float4*>(p);
-        xv[t].hi = *reinterpret_cast<const float4*>(p + 4);
+        const float* p = xr + (size_t)t * kBatchTile * ldx + k;
+        f.xlo[t] = *reinterpret_cast<const float4*>(p);
+        f.xhi[t] = *reinterpret_cast<const float4*>(p + 4);
       }
     };
-    uint4 w, gn;
-    X8 xv[NT];
-    load(k0, w, gn, xv);
-    for (int kb = k0; kb < k1; kb += 32) {
-      uint4 w2, gn2;
-      X8 xv2[NT];
-      load(kb + 32 < k1 ? kb + 32 : kb, w2, gn2, xv2);
-      const bf16x8 wb = __builtin_bit_cast(bf16x8, w);
+    auto mma = [&](int i, const Frag& f) {
       float gv[8];
       if constexpr (kNorm) {
-        const unsigned gu[4] = {gn.x, gn.y, gn.z, gn.w};
+        const unsigned gu[4] = {f.gn.x, f.gn.y, f.gn.z, f.gn.w};
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          gv[2 * i] = __builtin_bit_cast(float, gu[i] << 16);
-          gv[2 * i + 1] = __builtin_bit_cast(float, gu[i] & 0xffff0000u);
+        for (int j = 0; j < 4; j++) {
+          gv[2 * j] = __builtin_bit_cast(float, gu[j] << 16);
+          gv[2 * j + 1] = __builtin_bit_cast(float, gu[j] & 0xffff0000u);
         }
       }
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        float x[8] = {xv[t].lo.x, xv[t].lo.y, xv[t].lo.z, xv[t].lo.w, xv[t].hi.x, xv[t].hi.y, xv[t].hi.z, xv[t].hi.w};
+        float x[8] = {f.xlo[t].x, f.xlo[t].y, f.xlo[t].z, f.xlo[t].w, f.xhi[t].x, f.xhi[t].y, f.xhi[t].z, f.xhi[t].w};
         if constexpr (kNorm) {
 #pragma unroll
-          for (int i = 0; i < 8; i++) {
-            ss[t] += x[i] * x[i];
-            x[i] *= gv[i];
+          for (int j = 0; j < 8; j++) {
+            ss[i][t] += x[j] * x[j];
+            x[j] *= gv[j];
           }
         }
         unsigned ph[4], pm[4], pl[4];
+        split3(x, ph, pm, pl);
+        const bf16x8 h = __builtin_bit_cast(bf16x8, ph), m = __builtin_bit_cast(bf16x8, pm),
+                     l = __builtin_bit_cast(bf16x8, pl);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          unsigned h2[2], m2[2], l2[2];
-#pragma unroll
-          for (int j = 0; j < 2; j++) {
-            const float v = x[2 * i + j];
-            const unsigned hb = __builtin_bit_cast(unsigned, v) & 0xffff0000u;
-            const float r1 = v - __builtin_bit_cast(float, hb);
-            const unsigned mb = __builtin_bit_cast(unsigned, r1) & 0xffff0000u;
-            const float r2 = r1 - __builtin_bit_cast(float, mb);
-            h2[j] = hb;
-            m2[j] = mb;
-            l2[j] = __builtin_bit_cast(unsigned, r2) & 0xffff0000u;
-          }
-          ph[i] = h2[1] | (h2[0] >> 16);
-          pm[i] = m2[1] | (m2[0] >> 16);
-          pl[i] = l2[1] | (l2[0] >> 16);
+        for (int c = 0; c < CT; c++) {
+          const bf16x8 wb = __builtin_bit_cast(bf16x8, f.w[c]);
+          f4v& d = acc[i][t][c];
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h, wb, d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(m, wb, d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l, wb, d, 0, 0, 0);
         }
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ph), wb, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pm), wb, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pl), wb, acc[t], 0, 0, 0);
       }
-      w = w2;
-      gn = gn2;
+    };
+    if constexpr (SW == 1) {
+      const int k0 = wave * slice;
+      Frag cur;
+      load(k0, cur);
+      for (int kk = 0; kk < slice; kk += 32) {
+        Frag nxt;
+        load(k0 + (kk + 32 < slice ? kk + 32 : kk), nxt);
+        mma(0, cur);
+        cur = nxt;
+      }
+    } else {
+      for (int kk = 0; kk < slice; kk += 32) {
+        Frag f[SW];
 #pragma unroll
-      for (int t = 0; t < NT; t++) xv[t] = xv2[t];
+        for (int i = 0; i < SW; i++) load((wave * SW + i) * slice + kk, f[i]);
+#pragma unroll
+        for (int i = 0; i < SW; i++) mma(i, f[i]);
+      }
     }
   }
+  // A wave holding two slices adds them here: the first level of the tree.
 #pragma unroll
   for (int t = 0; t < NT; t++) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) red[wave][t][4 * g + r][r16] = acc[t][r];
+    for (int c = 0; c < CT; c++) {
+      f4v v = acc[0][t][c];
+      if constexpr (SW == 2) v = acc[0][t][c] + acc[1][t][c];
+#pragma unroll
+      for (int r = 0; r < 4; r++) red[wave][t][c][4 * g + r][r16] = v[r];
+    }
     if constexpr (kNorm) {
-      const float v = column_sum(ss[t], 16);
+      float v = column_sum(ss[0][t], 16);
+      if constexpr (SW == 2) v = v + column_sum(ss[1][t], 16);
       if (g == 0) sq[wave][t][r16] = v;
     }
   }
@@ -215,28 +266,29 @@ __global__ __launch_bounds__(512) void batch_proj(const BatchArgs* __restrict__ 
   // Epilogue: one thread per output unit (a column, or the column pair of a RoPE pair /
   // gate-up pair) of a stream below B.
   constexpr int unit = (E == kEpQkv || E == kEpGateUp) ? 2 : 1;
-  constexpr int per_row = kBatchTile / unit;
+  constexpr int per_row = kBatchTile * CT / unit;
+  auto tree = [&](auto at) {
+    float p[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) p[k] = SW == 2 ? at(k) : at(2 * k) + at(2 * k + 1);
+    return (p[0] + p[1]) + (p[2] + p[3]);
+  };
   for (int o = threadIdx.x; o < NT * kBatchTile * per_row; o += blockDim.x) {
     const int t = o / (kBatchTile * per_row);
     const int row = (o / per_row) % kBatchTile;
-    const int c = (o % per_row) * unit;
+    const int cc = (o % per_row) * unit;
+    const int c = cc / kBatchTile, col = cc % kBatchTile;
     const int b = (t0 + t) * kBatchTile + row;
     if (b >= a.streams) continue;
-    float s0 = red[0][t][row][c], s1 = unit == 2 ? red[0][t][row][c + 1] : 0.f;
-#pragma unroll
-    for (int w = 1; w < kProjWaves; w++) {
-      s0 += red[w][t][row][c];
-      if (unit == 2) s1 += red[w][t][row][c + 1];
-    }
+    float s0 = tree([&](int k) { return red[k][t][c][row][col]; });
+    float s1 = unit == 2 ? tree([&](int k) { return red[k][t][c][row][col + 1]; }) : 0.f;
     if constexpr (kNorm) {
-      float sum = sq[0][t][row];
-#pragma unroll
-      for (int w = 1; w < kProjWaves; w++) sum += sq[w][t][row];
+      const float sum = tree([&](int k) { return sq[k][t][row]; });
       const float scale = 1.0f / sqrtf(sum / (float)a.width + a.epsilon);
       s0 *= scale;
       s1 *= scale;
     }
-    const int n = n0 + c;
+    const int n = n0 + cc;
     float* xb = a.x + (size_t)b * a.width_p;
     if constexpr (E == kEpInput) {
       xb[n] = s0;

@@ -16,7 +16,10 @@ class Batch {
 
  private:
   template <int P> void launch_sequence();
-  int group_tiles(int N) const;
+  template <int P, int E, bool kNorm, int CT, int SW>
+  void project(const float* X, int ld, uint32_t woff, int N, uint32_t norm, int layer);
+  int group_tiles(int cols) const;
+  bool wide_qkv_ = false, wide_gateup_ = false;  // two column tiles per workgroup
   void launch() {
     if (prec_ == kFp32) launch_sequence<kFp32>();
     else launch_sequence<kBf16w>();
@@ -50,6 +53,8 @@ Batch::Batch(const st_config& config, const st_tensor* tensors, size_t count, in
   // groups (1, 2 or 4 tiles of 16) divide it.
   streams_p_ = streams <= 16 ? 16 : streams <= 32 ? 32 : (streams + 63) / 64 * 64;
   dim_ = c_.width / c_.heads;
+  wide_qkv_ = (3 * c_.width / kBatchTile) % 2 == 0;
+  wide_gateup_ = (2 * c_.ffn / kBatchTile) % 2 == 0;
   if (dim_ % 4) throw Error(ST_ERR_INVALID, "Batched streams need a head dimension that is a multiple of 4");
   int device = 0;
   HIP_CHECK(hipGetDevice(&device));
@@ -137,37 +142,49 @@ Batch::~Batch() {
 
 // Batch tiles per projection workgroup: the largest of 4, 2, 1 that still gives at least 256
 // workgroups (one per CU), so that narrow projections at small batches spread over the chip.
-int Batch::group_tiles(int N) const {
-  const int tiles = streams_p_ / kBatchTile, cols = N / kBatchTile;
+// `cols` is the number of column groups (N / (16 CT)).
+int Batch::group_tiles(int cols) const {
+  const int tiles = streams_p_ / kBatchTile;
   for (int nt = kGroupTiles; nt > 1; nt >>= 1)
     if (tiles % nt == 0 && cols * (tiles / nt) >= 256) return nt;
   return 1;
 }
 
+template <int P, int E, bool kNorm, int CT, int SW>
+void Batch::project(const float* X, int ld, uint32_t woff, int N, uint32_t norm, int layer) {
+  const int nt = group_tiles(N / (kBatchTile * CT));
+  const dim3 grid(N / (kBatchTile * CT), streams_p_ / kBatchTile / nt), block(64 * kSlices / SW);
+  if (nt == 4)
+    hipLaunchKernelGGL((batch_proj<P, E, kNorm, 4, CT, SW>), grid, block, 0, stream_, dargs_, X, ld, woff, ld, N, ld,
+                       norm, layer);
+  else if (nt == 2)
+    hipLaunchKernelGGL((batch_proj<P, E, kNorm, 2, CT, SW>), grid, block, 0, stream_, dargs_, X, ld, woff, ld, N, ld,
+                       norm, layer);
+  else
+    hipLaunchKernelGGL((batch_proj<P, E, kNorm, 1, CT, SW>), grid, block, 0, stream_, dargs_, X, ld, woff, ld, N, ld,
+                       norm, layer);
+}
+
+// The wide projections (QKV, gate/up) take two column tiles and two K-slices per wave, which
+// halves the X reads at large batches and still leaves many workgroups at small ones; the
+// narrow ones (input, OUT, down: d outputs) keep one of each for parallelism. The choice
+// depends on the shape only, never on B.
 template <int P>
 void Batch::launch_sequence() {
   const BatchArgs& a = args_;
-  const int tiles = streams_p_ / kBatchTile;
-  auto proj = [&](auto k1, auto k2, auto k4, const float* X, int ld, uint32_t woff, int N, uint32_t norm, int layer) {
-    const int nt = group_tiles(N);
-    const dim3 grid(N / kBatchTile, tiles / nt), block(64 * kProjWaves);
-    if (nt == 4) hipLaunchKernelGGL(k4, grid, block, 0, stream_, dargs_, X, ld, woff, ld, N, ld, norm, layer);
-    else if (nt == 2) hipLaunchKernelGGL(k2, grid, block, 0, stream_, dargs_, X, ld, woff, ld, N, ld, norm, layer);
-    else hipLaunchKernelGGL(k1, grid, block, 0, stream_, dargs_, X, ld, woff, ld, N, ld, norm, layer);
-  };
-#define STAMD_PROJ(E, NORM) batch_proj<P, E, NORM, 1>, batch_proj<P, E, NORM, 2>, batch_proj<P, E, NORM, 4>
   const int d = c_.width, F = c_.ffn;
-  proj(STAMD_PROJ(kEpInput, false), a.in, a.features_p, a.w_input, d, 0u, 0);
+  project<P, kEpInput, false, 1, 1>(a.in, a.features_p, a.w_input, d, 0u, 0);
   for (int l = 0; l < c_.layers; l++) {
     const LayerWeights& w = a.layer[l];
-    proj(STAMD_PROJ(kEpQkv, true), a.x, a.width_p, w.qkv, 3 * d, w.norm1, l);
+    if (wide_qkv_) project<P, kEpQkv, true, 2, 2>(a.x, a.width_p, w.qkv, 3 * d, w.norm1, l);
+    else project<P, kEpQkv, true, 1, 1>(a.x, a.width_p, w.qkv, 3 * d, w.norm1, l);
     hipLaunchKernelGGL(batch_attention, dim3(streams_ * c_.heads), dim3(kAttnThreads), (size_t)c_.window * 4, stream_,
                        dargs_, l);
-    proj(STAMD_PROJ(kEpOut, false), a.attn, a.width_p, w.out, d, 0u, l);
-    proj(STAMD_PROJ(kEpGateUp, true), a.x, a.width_p, w.gateup, 2 * F, w.norm2, l);
-    proj(STAMD_PROJ(kEpDown, false), a.act, a.ffn_p, w.down, d, 0u, l);
+    project<P, kEpOut, false, 1, 1>(a.attn, a.width_p, w.out, d, 0u, l);
+    if (wide_gateup_) project<P, kEpGateUp, true, 2, 2>(a.x, a.width_p, w.gateup, 2 * F, w.norm2, l);
+    else project<P, kEpGateUp, true, 1, 1>(a.x, a.width_p, w.gateup, 2 * F, w.norm2, l);
+    project<P, kEpDown, false, 1, 1>(a.act, a.ffn_p, w.down, d, 0u, l);
   }
-#undef STAMD_PROJ
   hipLaunchKernelGGL(batch_final<P>, dim3(streams_), dim3(64), 0, stream_, dargs_);
   HIP_CHECK(hipGetLastError());
 }
