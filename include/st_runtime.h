@@ -150,6 +150,23 @@ int st_runtime_device_run(st_runtime* runtime, const float* inputs, size_t count
 int st_runtime_phase_times(st_runtime* runtime, const float* input, double* us, size_t cap,
                            size_t* count);
 
+/* std::map<std::string, std::vector<float>> Runtime::traceStep(const float* input) -
+ * src/cuda/Runtime.cu:476-546; staged backend (ST_BACKEND_CUDA) only, like the reference.
+ * Runs one real step (advancing the stream exactly like st_runtime_step) and records the
+ * named operation/cast boundaries of the reference's trace: "input.operand", ".pre_cast",
+ * ".linear", "input", and per layer "layers.{l}.norm1.*", ".q|k|v.*", ".q", ".k", ".v",
+ * ".attention", ".out.*", ".attention_residual", ".norm2.*", ".gate.*", ".up.*",
+ * ".activation", ".down.*", ".hidden", then "final_norm.*" and "score.*". The phase outputs
+ * (input, q, k, v, attention, attention_residual, activation, hidden, score.linear) are the
+ * step's own values; the per-operation entries (.operand, .pre_cast, .norm, .linear) are
+ * recomputed from the phase inputs by diagnostic kernels.
+ * names receives a JSON object {"name": [offset, count], ...} (at most names_cap bytes,
+ * NUL-terminated, full length in *names_needed); values receives the concatenated vectors
+ * (values_cap must hold all; the total is written to *values_count). With names_cap and
+ * values_cap both 0 only the sizes are written and no step runs. */
+int st_runtime_trace_step(st_runtime* runtime, const float* input, char* names, size_t names_cap,
+                          size_t* names_needed, float* values, size_t values_cap, size_t* values_count);
+
 /* Json Runtime::info() const - src/cuda/Runtime.cu:570-594, as a JSON string. Writes at
  * most cap bytes (NUL-terminated) and the full length to *needed. */
 int st_runtime_info_json(st_runtime* runtime, char* buffer, size_t cap, size_t* needed);

@@ -5,6 +5,7 @@
 // device-held position and epoch. Mirrors Stream::Runtime::Impl (src/cuda/Runtime.cu:167-653) behind a C ABI.
 #include "step_phases.hpp"
 #include "batch_kernels.hpp"
+#include "diag_kernels.hpp"
 #include "../../include/st_runtime.h"
 
 #include <hip/hip_runtime.h>
@@ -199,6 +200,9 @@ class Runtime {
   double device_trace(const float* inputs, size_t count, double* per_event);
   double device_run(const float* inputs, size_t count, bool reset_first, double* per_event);
   size_t phase_times(const float* input, double* us, size_t cap);
+  // traceStep: names and sizes of the trace entries in output order (fixed by the config).
+  std::vector<std::pair<std::string, size_t>> trace_layout() const;
+  std::vector<std::pair<std::string, std::vector<float>>> trace_step(const float* input);
   std::string info();
 
  private:
@@ -881,6 +885,175 @@ double Runtime::device_run(const float* inputs, size_t count, bool reset_first, 
   return total_ms * 1000.0 / count;
 }
 
+// Trace of one step (Runtime::traceStep, src/cuda/Runtime.cu:476-546), on the staged backend
+// like the reference. The step runs in the phase kernels, one launch at a time, so it leaves
+// exactly the state and score of an ordinary step; after each phase its output vector (x, q,
+// k, v, attention, activation, hidden, score) is read back. The per-operation entries that the
+// phases keep internal (".operand", ".pre_cast", ".norm", ".linear") are recomputed by the
+// diagnostic kernels from the captured phase inputs.
+std::vector<std::pair<std::string, size_t>> Runtime::trace_layout() const {
+  const size_t d = c_.width, F = c_.ffn, f = c_.features;
+  std::vector<std::pair<std::string, size_t>> l;
+  auto linear = [&](const std::string& n, size_t rows, size_t cols) {
+    l.push_back({n + ".operand", cols});
+    l.push_back({n + ".pre_cast", rows});
+    l.push_back({n + ".linear", rows});
+  };
+  auto norm = [&](const std::string& n) {
+    l.push_back({n + ".operand", d});
+    l.push_back({n + ".pre_cast", d});
+    l.push_back({n + ".norm", d});
+  };
+  linear("input", d, f);
+  l.push_back({"input", d});
+  for (int layer = 0; layer < c_.layers; layer++) {
+    const std::string p = "layers." + std::to_string(layer) + ".";
+    norm(p + "norm1");
+    linear(p + "q", d, d);
+    linear(p + "k", d, d);
+    linear(p + "v", d, d);
+    l.push_back({p + "q", d});
+    l.push_back({p + "k", d});
+    l.push_back({p + "v", d});
+    l.push_back({p + "attention", d});
+    linear(p + "out", d, d);
+    l.push_back({p + "attention_residual", d});
+    norm(p + "norm2");
+    linear(p + "gate", F, d);
+    linear(p + "up", F, d);
+    l.push_back({p + "activation", F});
+    linear(p + "down", d, F);
+    l.push_back({p + "hidden", d});
+  }
+  norm("final_norm");
+  linear("score", 1, d);
+  return l;
+}
+
+std::vector<std::pair<std::string, std::vector<float>>> Runtime::trace_step(const float* input) {
+  if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
+  if (opt_.backend != ST_BACKEND_CUDA) throw Error(ST_ERR_INVALID, "traceStep requires the staged backend (CUDA)");
+  if (!input) throw Error(ST_ERR_INVALID, "Null input");
+  const int d = c_.width, F = c_.ffn, f = c_.features;
+  const StepArgs& a = args_;
+  std::map<std::string, std::vector<float>> t;
+  const size_t wide = (size_t)std::max({3 * d, 2 * F, f, d});
+  DeviceBuffer operand, pre, out;
+  operand.alloc(wide * 4);
+  pre.alloc(wide * 4);
+  out.alloc(wide * 4);
+  float* dop = reinterpret_cast<float*>(operand.ptr);
+  float* dpre = reinterpret_cast<float*>(pre.ptr);
+  float* dout = reinterpret_cast<float*>(out.ptr);
+  auto fetch = [&](const float* src, size_t n) {
+    std::vector<float> v(n);
+    HIP_CHECK(hipMemcpy(v.data(), src, n * 4, hipMemcpyDeviceToHost));
+    return v;
+  };
+  auto tagged = [&](uint32_t off, size_t n) {
+    std::vector<unsigned long long> w(n);
+    HIP_CHECK(hipMemcpy(w.data(), a.tagged + off, n * 8, hipMemcpyDeviceToHost));
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; i++) {
+      const uint32_t bits = (uint32_t)(w[i] & 0xffffffffull);
+      std::memcpy(&v[i], &bits, 4);
+    }
+    return v;
+  };
+  auto run_phase = [&](int ph) {
+    dispatch([&](auto P, auto A) {
+      const int resident = std::min(grid_, legal_blocks_);
+      const int grid = ph == 5 * c_.layers + 1 ? 1 : resident;
+      hipLaunchKernelGGL((phase_kernel<P.value, A.value>), dim3(grid), dim3(kThreads), 0, stream_, dargs_, ph);
+      return 0;
+    });
+    HIP_CHECK(hipGetLastError());
+    sync();
+  };
+  // pre_cast / cast of one projection of `operand` (host vector) over arena rows.
+  auto linear = [&](const std::string& n, const std::vector<float>& v, uint32_t woff, int ld, int first, int stride,
+                    int rows, bool final) {
+    t[n + ".operand"] = v;
+    HIP_CHECK(hipMemcpy(dop, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+    dispatch([&](auto P, auto) {
+      hipLaunchKernelGGL((diag_linear<P.value>), dim3((rows + 3) / 4), dim3(256), 0, stream_, a.weights, woff, ld,
+                         first, stride, rows, (int)v.size(), dop, dpre, dout, final ? 1 : 0);
+      return 0;
+    });
+    HIP_CHECK(hipGetLastError());
+    sync();
+    t[n + ".pre_cast"] = fetch(dpre, rows);
+    t[n + ".linear"] = fetch(dout, rows);
+    return t[n + ".linear"];
+  };
+  auto norm = [&](const std::string& n, const std::vector<float>& x, uint32_t w_norm) {
+    t[n + ".operand"] = x;
+    HIP_CHECK(hipMemcpy(dop, x.data(), x.size() * 4, hipMemcpyHostToDevice));
+    dispatch([&](auto P, auto) {
+      hipLaunchKernelGGL((diag_norm<P.value>), dim3(1), dim3(256), 0, stream_, a.weights, w_norm, d, c_.epsilon, dop,
+                         dpre, dout);
+      return 0;
+    });
+    HIP_CHECK(hipGetLastError());
+    sync();
+    t[n + ".pre_cast"] = fetch(dpre, d);
+    t[n + ".norm"] = fetch(dout, d);
+    return t[n + ".norm"];
+  };
+
+  std::memcpy(host_in_.ptr, input, (size_t)f * 4);
+  HIP_CHECK(hipMemcpyAsync(a.scratch + a.s_input, host_in_.ptr, (size_t)a.features_p * 4, hipMemcpyHostToDevice,
+                           stream_));
+  sync();
+  linear("input", std::vector<float>(input, input + f), a.w_input, a.features_p, 0, 1, d, false);
+  run_phase(0);
+  std::vector<float> x = tagged(a.t_x, d);
+  t["input"] = x;
+  for (int l = 0; l < c_.layers; l++) {
+    const std::string p = "layers." + std::to_string(l) + ".";
+    const LayerWeights& w = a.layer[l];
+    const std::vector<float> n1 = norm(p + "norm1", x, w.norm1);
+    linear(p + "q", n1, w.qkv, a.width_p, 0, 1, d, false);
+    linear(p + "k", n1, w.qkv, a.width_p, d, 1, d, false);
+    linear(p + "v", n1, w.qkv, a.width_p, 2 * d, 1, d, false);
+    run_phase(1 + 5 * l);
+    t[p + "q"] = tagged(a.t_q, d);
+    t[p + "k"] = tagged(a.t_k, d);
+    t[p + "v"] = tagged(a.t_v, d);
+    run_phase(2 + 5 * l);
+    const std::vector<float> attention = tagged(a.t_attn, d);
+    t[p + "attention"] = attention;
+    linear(p + "out", attention, w.out, a.width_p, 0, 1, d, false);
+    run_phase(3 + 5 * l);
+    x = tagged(a.t_x, d);
+    t[p + "attention_residual"] = x;
+    const std::vector<float> n2 = norm(p + "norm2", x, w.norm2);
+    linear(p + "gate", n2, w.gateup, a.width_p, 0, 2, F, false);
+    linear(p + "up", n2, w.gateup, a.width_p, 1, 2, F, false);
+    run_phase(4 + 5 * l);
+    const std::vector<float> act = tagged(a.t_act, F);
+    t[p + "activation"] = act;
+    linear(p + "down", act, w.down, a.ffn_p, 0, 1, d, false);
+    run_phase(5 + 5 * l);
+    x = tagged(a.t_x, d);
+    t[p + "hidden"] = x;
+  }
+  const std::vector<float> fin = norm("final_norm", x, a.w_final_norm);
+  t["score.operand"] = fin;
+  run_phase(5 * c_.layers + 1);
+  check_device_error();
+  const std::vector<float> score = fetch(a.scratch + a.s_score, 1);
+  t["score.pre_cast"] = score;  // the score has no cast
+  t["score.linear"] = score;
+  std::vector<std::pair<std::string, std::vector<float>>> result;
+  for (const auto& [name, n] : trace_layout()) {
+    auto it = t.find(name);
+    if (it == t.end() || it->second.size() != n) throw Error(ST_ERR_DEVICE, "Trace entry missing: " + name);
+    result.push_back({name, std::move(it->second)});
+  }
+  return result;
+}
+
 // One fused step with wall-clock stamps. For each phase and workgroup writes kStamps times
 // in microseconds since workgroup 0 started the step (slots as in stamp()); 0 where not
 // recorded; then the end of the step.
@@ -1070,6 +1243,36 @@ int st_runtime_phase_times(st_runtime* r, const float* input, double* us, size_t
     if (!r || !input || (!us && cap)) throw stamd::Error(ST_ERR_INVALID, "Null argument");
     size_t n = r->impl->phase_times(input, us, cap);
     if (count) *count = n;
+  });
+}
+
+int st_runtime_trace_step(st_runtime* r, const float* input, char* names, size_t names_cap, size_t* names_needed,
+                          float* values, size_t values_cap, size_t* values_count) {
+  return guarded([&] {
+    if (!r || (!names && names_cap) || (!values && values_cap)) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    const auto layout = r->impl->trace_layout();
+    std::ostringstream o;
+    size_t total = 0;
+    o << "{";
+    for (size_t i = 0; i < layout.size(); i++) {
+      o << (i ? ", " : "") << "\"" << layout[i].first << "\": [" << total << ", " << layout[i].second << "]";
+      total += layout[i].second;
+    }
+    o << "}";
+    if (values_count) *values_count = total;
+    if (names_cap == 0 && values_cap == 0) {  // size query: no step
+      write_string(o.str(), nullptr, 0, names_needed);
+      return;
+    }
+    if (!input) throw stamd::Error(ST_ERR_INVALID, "Null input");
+    if (values_cap < total) throw stamd::Error(ST_ERR_INVALID, "Trace value buffer too small");
+    const auto trace = r->impl->trace_step(input);
+    size_t off = 0;
+    for (const auto& [name, v] : trace) {
+      std::memcpy(values + off, v.data(), v.size() * 4);
+      off += v.size();
+    }
+    write_string(o.str(), names, names_cap, names_needed);
   });
 }
 

@@ -99,6 +99,8 @@ def library(path: os.PathLike | None = None) -> ctypes.CDLL:
     lib.st_runtime_device_trace.argtypes = [P, F, ctypes.c_size_t, D, D]
     lib.st_runtime_device_run.argtypes = [P, F, ctypes.c_size_t, ctypes.c_int32, D, D]
     lib.st_runtime_phase_times.argtypes = [P, F, D, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+    lib.st_runtime_trace_step.argtypes = [P, F, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t), F,
+                                          ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_runtime_info_json.argtypes = [P, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_probe_json.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_last_error.argtypes = []
@@ -114,6 +116,7 @@ def library(path: os.PathLike | None = None) -> ctypes.CDLL:
     for name in ('st_batch_create', 'st_batch_step', 'st_batch_reset', 'st_batch_snapshot', 'st_batch_device_run',
                  'st_runtime_create', 'st_runtime_step', 'st_runtime_reset', 'st_runtime_stop',
                  'st_runtime_snapshot', 'st_runtime_device_trace', 'st_runtime_device_run', 'st_runtime_phase_times',
+                 'st_runtime_trace_step',
                  'st_runtime_info_json',
                  'st_probe_json'):
         getattr(lib, name).restype = ctypes.c_int
@@ -269,6 +272,22 @@ class Runtime:
                                           ctypes.byref(count)))
         phases = 5 * self.config.layers + 2
         return out[:-1].reshape(phases, -1, 8), float(out[-1])
+
+    def trace_step(self, event) -> dict:
+        """Runtime::traceStep (staged backend): one real step; {name: FP32 array} of the
+        operation/cast boundaries, in the reference's naming."""
+        x = np.ascontiguousarray(event, dtype=np.float32)
+        if x.size != self.config.features:
+            raise ValueError('event must hold `features` floats')
+        lib = library()
+        needed, total = ctypes.c_size_t(0), ctypes.c_size_t(0)
+        _check(lib.st_runtime_trace_step(self._handle(), _fptr(x), None, 0, ctypes.byref(needed), None, 0,
+                                         ctypes.byref(total)))
+        names = ctypes.create_string_buffer(needed.value)
+        values = np.empty(total.value, dtype=np.float32)
+        _check(lib.st_runtime_trace_step(self._handle(), _fptr(x), names, needed.value, ctypes.byref(needed),
+                                         _fptr(values), total.value, ctypes.byref(total)))
+        return {name: values[o:o + n].copy() for name, (o, n) in json.loads(names.value.decode()).items()}
 
     def info(self) -> dict:
         return _json(library().st_runtime_info_json, self._handle())

@@ -243,3 +243,94 @@ def test_vendor_backends_match_oracle_and_graph_replays_match_eager(name, steps,
     for a, b, o in zip(st0[1:], st1[1:], (ok, ov, oh)):
         np.testing.assert_array_equal(a, b)
         assert numerical.fp32_strict_failures(a, o, **STRICT) == 0, float(np.abs(a - o).max())
+
+
+@pytest.mark.parametrize('fixture', ['main-mixed', 'small-fp32'])
+def test_trace_step_preserves_execution(golden, fixture):
+    # tests/Lifecycle.cu:108-137: traced steps give the scores and leave the state of ordinary
+    # steps, bit for bit.
+    g = golden(fixture)
+    c = g.config
+    with runtime(g.checkpoint, Backend.CUDA, 4) as rt:
+        scores = [rt.step(e) for e in g.trace[:12]]
+        state = rt.snapshot()
+        rt.reset()
+        for i, e in enumerate(g.trace[:12]):
+            trace = rt.trace_step(e)
+            assert trace['layers.0.attention'].shape == (c.width,)
+            assert trace['score.linear'][0] == scores[i]
+            if g.checkpoint.mixed:
+                for name, v in trace.items():
+                    # every cast point is FP16; the raw event and the uncast score are not
+                    if not name.endswith('.pre_cast') and name != 'input.operand' and not name.startswith('score.'):
+                        assert np.array_equal(v, v.astype(np.float16).astype(np.float32)), name
+        traced = rt.snapshot()
+    assert traced[0] == state[0]
+    for a, b in zip(traced[1:], state[1:]):
+        np.testing.assert_array_equal(a, b)
+
+
+def _rms(x, g, eps):
+    x = x.astype(np.float64)
+    return x / np.sqrt(np.mean(x * x) + eps) * g
+
+
+def test_trace_entries_satisfy_the_model_equations():
+    # The diagnostic entries against the model's closed forms (float64 numpy), and the phase
+    # outputs against the carried state.
+    c = ModelConfig(2, 128, 4, 256, 16, 96)
+    w = synthetic_checkpoint(c, seed=21)
+    events = _stream(c, 21, 20)
+    tol = dict(atol=2e-6, rtol=2e-5)
+    with runtime((c, w, False), Backend.CUDA, 0) as rt:
+        for e in events[:19]:
+            rt.step(e)
+        t = rt.trace_step(events[19])
+        pos, keys, values, hidden = rt.snapshot()
+    position, slot = pos - 1, (pos - 1) % c.window
+    lin = lambda name, m, v: np.testing.assert_allclose(t[name + '.linear'], m @ v.astype(np.float64), **tol)
+    np.testing.assert_array_equal(t['input.operand'], events[19])
+    lin('input', w['input'], events[19])
+    np.testing.assert_allclose(t['input'], t['input.linear'], **tol)
+    x = t['input']
+    dh = c.dim
+    inv = 10000.0 ** (-np.arange(0, dh, 2, dtype=np.float32) / dh)
+    ang = np.float32(position) * inv.astype(np.float32)
+    co, si = np.cos(ang.astype(np.float64)), np.sin(ang.astype(np.float64))
+    for l in range(c.layers):
+        p = f'layers.{l}.'
+        np.testing.assert_array_equal(t[p + 'norm1.operand'], x)
+        np.testing.assert_allclose(t[p + 'norm1.norm'], _rms(x, w[p + 'norm1'], c.epsilon), **tol)
+        n1 = t[p + 'norm1.norm']
+        for m in ('q', 'k', 'v'):
+            np.testing.assert_array_equal(t[p + m + '.operand'], n1)
+            lin(p + m, w[p + m], n1)
+        for m in ('q', 'k'):
+            a = t[p + m + '.linear'].reshape(c.heads, dh // 2, 2).astype(np.float64)
+            rot = np.stack([a[..., 0] * co - a[..., 1] * si, a[..., 0] * si + a[..., 1] * co], -1)
+            np.testing.assert_allclose(t[p + m], rot.reshape(-1), **tol)
+        np.testing.assert_allclose(t[p + 'v'], t[p + 'v.linear'], **tol)
+        np.testing.assert_array_equal(t[p + 'k'].reshape(c.heads, dh), keys[l, :, slot])
+        np.testing.assert_array_equal(t[p + 'v'].reshape(c.heads, dh), values[l, :, slot])
+        lin(p + 'out', w[p + 'out'], t[p + 'attention'])
+        np.testing.assert_allclose(t[p + 'attention_residual'], x + t[p + 'out.linear'], **tol)
+        x = t[p + 'attention_residual']
+        np.testing.assert_allclose(t[p + 'norm2.norm'], _rms(x, w[p + 'norm2'], c.epsilon), **tol)
+        for m in ('gate', 'up'):
+            lin(p + m, w[p + m], t[p + 'norm2.norm'])
+        gv, uv = t[p + 'gate.linear'].astype(np.float64), t[p + 'up.linear']
+        np.testing.assert_allclose(t[p + 'activation'], gv / (1 + np.exp(-gv)) * uv, **tol)
+        lin(p + 'down', w[p + 'down'], t[p + 'activation'])
+        np.testing.assert_allclose(t[p + 'hidden'], x + t[p + 'down.linear'], **tol)
+        np.testing.assert_array_equal(t[p + 'hidden'], hidden[l])
+        x = t[p + 'hidden']
+    np.testing.assert_allclose(t['final_norm.norm'], _rms(x, w['final_norm'], c.epsilon), **tol)
+    np.testing.assert_allclose(t['score.linear'], w['score'] @ t['final_norm.norm'].astype(np.float64), **tol)
+
+
+def test_trace_step_requires_staged_backend():
+    c = ModelConfig(1, 64, 4, 128, 8, 32)
+    w = synthetic_checkpoint(c, seed=22)
+    with runtime((c, w, False), Backend.FUSED, 0) as rt:
+        with pytest.raises(RuntimeError, match='staged'):
+            rt.trace_step(np.zeros(c.features, dtype=np.float32))
