@@ -13,7 +13,8 @@ already resident in HBM). The library synchronizes its stream before and after t
 launches. One JSON line is printed.
 
 Secondary measurements (skipped with --quick) go under "extra": host-service latency through
-step(), the device loop, the persistent worker, the vendor GEMV baseline (rocBLAS projections
+step(), the device loop, the persistent worker, the transport floors (mailbox ping-pong, empty
+launch, empty graph, copy), the vendor GEMV baseline (rocBLAS projections
 in a captured graph) on the same workload, B independent streams over shared weights
 (Main, bfloat16 weights, W=128, B in 1, 16, 64, 256; --batched runs only that), and the Main
 window sweep (W in 32..512, bfloat16 weights and mixed mode).
@@ -38,7 +39,8 @@ for p in (ROOT, ROOT / 'streaming-transformer_amd'):
     if str(p) not in sys.path:
         sys.path.insert(0, str(p))
 
-from streamtx import Backend, BatchRuntime, ModelConfig, Runtime, RuntimeOptions, WeightStorage, synthetic_checkpoint  # noqa: E402
+from streamtx import (Backend, BatchRuntime, ModelConfig, Runtime, RuntimeOptions, WeightStorage,  # noqa: E402
+                     synthetic_checkpoint, transport_bench)
 
 CONFIGS = {
     'small': (ModelConfig(4, 256, 4, 1024, 64, 256), 0),
@@ -247,6 +249,9 @@ def main():
             _, vper = rt.device_run(events[fill:fill + min(args.steps, 256)])
         extra['vendor_gemv_graph_p50_us'] = nearest_rank(vper, 0.5)
     if not args.quick:
+        # Transport floors under a step (the reference's transportBench modes).
+        extra['transport_p50_us'] = {m: round(transport_bench(m, 2000)['p50_us'], 2)
+                                     for m in ('ping-pong', 'gpu-ping', 'empty', 'empty-graph', 'copy')}
         extra['batched'] = batched_streams()
         extra['window_sweep'] = window_sweep()
 

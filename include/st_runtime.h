@@ -171,6 +171,17 @@ int st_runtime_trace_step(st_runtime* runtime, const float* input, char* names, 
  * most cap bytes (NUL-terminated) and the full length to *needed. */
 int st_runtime_info_json(st_runtime* runtime, char* buffer, size_t cap, size_t* needed);
 
+/* Json transportBench(mode, count, backoff, output) - include/Runtime.hpp:46,
+ * src/cuda/Runtime.cu:703-814: `count` round trips of one transport mode, "ping-pong"
+ * (host request, resident one-thread kernel answers through coherent pinned memory),
+ * "gpu-ping" (the kernel initiates, the host answers), "empty" / "empty-graph" (an empty
+ * kernel launched or replayed from a hipGraph, then synchronized) or "copy" (128 bytes in, an
+ * echo kernel, 128 bytes out). Writes per-sample CSV rows to csv_path unless it is NULL or
+ * empty, and the JSON report (p50/p99/worst microseconds, failures) like info_json. Checksum
+ * failures return ST_ERR_NUMERIC. */
+int st_transport_bench(const char* mode, uint64_t count, int32_t backoff, const char* csv_path, char* report,
+                       size_t cap, size_t* needed);
+
 /* Json probe() - src/cuda/Runtime.cu:134-161, as a JSON string. */
 int st_probe_json(char* buffer, size_t cap, size_t* needed);
 

@@ -1151,6 +1151,208 @@ static int guarded(F&& f) {
   }
 }
 
+namespace stamd {
+
+// ---------------------------------------------------------------------------------------------
+// Transport microbenchmarks (Stream::transportBench, src/cuda/Runtime.cu:667-814): the floors
+// under a step. "ping-pong": the host releases a request through coherent pinned memory and a
+// resident one-thread kernel answers with a checksum of 32 mapped floats; "gpu-ping": the
+// kernel initiates and the host answers; "empty" / "empty-graph": an empty kernel launched
+// (or replayed from a hipGraph) and synchronized; "copy": 128 bytes host-to-device, an echo
+// kernel, 128 bytes back, synchronized and compared.
+
+struct alignas(64) PingBox {
+  alignas(64) unsigned long long request;
+  alignas(64) unsigned long long completion;
+  alignas(64) unsigned long long exited;
+  alignas(64) unsigned long long checksum;
+};
+
+__global__ void transport_empty_kernel() {}
+
+__global__ void transport_echo_kernel(const float* in, float* out, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = in[i];
+}
+
+// One thread; every wait ends within `idle_ticks` of the wall clock (then the kernel marks
+// itself exited and returns).
+__global__ void transport_ping_kernel(PingBox* box, const float* input, unsigned long long count, int backoff,
+                                      unsigned long long idle_ticks, int gpu_initiated, unsigned long long* ticks,
+                                      int* errors) {
+  if (threadIdx.x || blockIdx.x) return;
+  for (unsigned long long seq = 1; seq <= count; seq++) {
+    const unsigned long long start = wall_clock64();
+    if (gpu_initiated) {
+      __hip_atomic_store(&box->checksum, seq * 2654435761ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(&box->request, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+      while (__hip_atomic_load(&box->completion, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) != seq) {
+        if (wall_clock64() - start > idle_ticks) {
+          __hip_atomic_store(&box->exited, 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+          return;
+        }
+        if (backoff) __builtin_amdgcn_s_sleep(8);
+      }
+      if (__hip_atomic_load(&box->checksum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != ((seq * 2654435761ull) ^ 0xabcdefull))
+        (*errors)++;
+    } else {
+      while (__hip_atomic_load(&box->request, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) != seq) {
+        if (wall_clock64() - start > idle_ticks) {
+          __hip_atomic_store(&box->exited, 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+          return;
+        }
+        if (backoff) __builtin_amdgcn_s_sleep(8);
+      }
+      unsigned long long sum = 0;
+      for (int i = 0; i < 32; i++) sum += __builtin_bit_cast(unsigned, input[i]);
+      __hip_atomic_store(&box->checksum, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(&box->completion, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    ticks[seq - 1] = wall_clock64() - start;
+  }
+  __hip_atomic_store(&box->exited, 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+std::string transport_bench(const std::string& mode, uint64_t count, bool backoff, const char* csv_path) {
+  const bool interactive = mode == "ping-pong" || mode == "gpu-ping";
+  if (!interactive && mode != "empty" && mode != "empty-graph" && mode != "copy")
+    throw Error(ST_ERR_INVALID, "Unknown transport mode: " + mode);
+  if (count == 0 || count > (1ull << 24)) throw Error(ST_ERR_INVALID, "Transport count must be 1 .. 2^24");
+  const std::string environment = probe_json();
+  int device = 0, wall_khz = 100000;
+  HIP_CHECK(hipGetDevice(&device));
+  HIP_CHECK(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, device));
+  hipStream_t stream;
+  HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+  struct StreamGuard {
+    hipStream_t s;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t e = nullptr;
+    ~StreamGuard() {
+      (void)hipStreamSynchronize(s);
+      if (e) (void)hipGraphExecDestroy(e);
+      if (g) (void)hipGraphDestroy(g);
+      (void)hipStreamDestroy(s);
+    }
+  } guard{stream};
+  MappedBuffer box_buf, in_buf;
+  box_buf.alloc(sizeof(PingBox));
+  in_buf.alloc(32 * 4);
+  PingBox* box = reinterpret_cast<PingBox*>(box_buf.ptr);
+  float* input = reinterpret_cast<float*>(in_buf.ptr);
+  PinnedBuffer host_in, host_out;
+  host_in.alloc(128);
+  host_out.alloc(128);
+  DeviceBuffer d_in, d_out, d_ticks, d_errors;
+  d_in.alloc(128);
+  d_out.alloc(128);
+  d_ticks.alloc(count * 8);
+  d_errors.alloc(4);
+  HIP_CHECK(hipMemset(d_errors.ptr, 0, 4));
+  HIP_CHECK(hipMemset(d_ticks.ptr, 0, count * 8));
+  if (mode == "empty-graph") {
+    HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    hipLaunchKernelGGL(transport_empty_kernel, dim3(1), dim3(1), 0, stream);
+    HIP_CHECK(hipStreamEndCapture(stream, &guard.g));
+    HIP_CHECK(hipGraphInstantiate(&guard.e, guard.g, nullptr, nullptr, 0));
+  }
+  if (interactive) {
+    const unsigned long long idle = (unsigned long long)wall_khz * 1000ull * 30ull;  // 30 s per wait
+    hipLaunchKernelGGL(transport_ping_kernel, dim3(1), dim3(1), 0, stream, reinterpret_cast<PingBox*>(box_buf.dev),
+                       reinterpret_cast<const float*>(in_buf.dev), (unsigned long long)count, backoff ? 1 : 0, idle,
+                       mode == "gpu-ping" ? 1 : 0, reinterpret_cast<unsigned long long*>(d_ticks.ptr),
+                       reinterpret_cast<int*>(d_errors.ptr));
+    HIP_CHECK(hipGetLastError());
+  }
+  auto wait = [&](unsigned long long* word, unsigned long long seq) {
+    const auto start = std::chrono::steady_clock::now();
+    uint64_t polls = 0;
+    while (__atomic_load_n(word, __ATOMIC_ACQUIRE) != seq) {
+      if (backoff) std::this_thread::yield();
+      if ((++polls & 0xffff) == 0) {
+        if (__atomic_load_n(&box->exited, __ATOMIC_ACQUIRE))
+          throw Error(ST_ERR_STATE, "Ping kernel exited before the request or acknowledgement");
+        if (std::chrono::steady_clock::now() - start > std::chrono::seconds(60))
+          throw Error(ST_ERR_STATE, "Ping host timeout");
+      }
+    }
+  };
+  std::vector<double> samples(count);
+  uint64_t failed = 0;
+  const auto begin = std::chrono::steady_clock::now();
+  float* hin = reinterpret_cast<float*>(host_in.ptr);
+  for (uint64_t seq = 1; seq <= count; seq++) {
+    unsigned long long checksum = 0;
+    for (int i = 0; i < 32; i++) {
+      const float v = (float)(seq % 1024 + i);
+      input[i] = v;
+      hin[i] = v;
+      uint32_t bits;
+      std::memcpy(&bits, &v, 4);
+      checksum += bits;
+    }
+    const auto start = std::chrono::steady_clock::now();
+    if (mode == "gpu-ping") {
+      wait(&box->request, seq);
+      const unsigned long long got = __atomic_load_n(&box->checksum, __ATOMIC_RELAXED);
+      if (got != seq * 2654435761ull) failed++;
+      __atomic_store_n(&box->checksum, got ^ 0xabcdefull, __ATOMIC_RELAXED);
+      __atomic_store_n(&box->completion, seq, __ATOMIC_RELEASE);
+    } else if (mode == "ping-pong") {
+      __atomic_store_n(&box->request, seq, __ATOMIC_RELEASE);
+      wait(&box->completion, seq);
+      if (__atomic_load_n(&box->checksum, __ATOMIC_RELAXED) != checksum) failed++;
+    } else {
+      if (mode == "empty") {
+        hipLaunchKernelGGL(transport_empty_kernel, dim3(1), dim3(1), 0, stream);
+      } else if (mode == "empty-graph") {
+        HIP_CHECK(hipGraphLaunch(guard.e, stream));
+      } else {
+        HIP_CHECK(hipMemcpyAsync(d_in.ptr, host_in.ptr, 128, hipMemcpyHostToDevice, stream));
+        hipLaunchKernelGGL(transport_echo_kernel, dim3(1), dim3(32), 0, stream, reinterpret_cast<const float*>(d_in.ptr),
+                           reinterpret_cast<float*>(d_out.ptr), 32);
+        HIP_CHECK(hipMemcpyAsync(host_out.ptr, d_out.ptr, 128, hipMemcpyDeviceToHost, stream));
+      }
+      HIP_CHECK(hipGetLastError());
+      HIP_CHECK(hipStreamSynchronize(stream));
+      if (mode == "copy" && std::memcmp(host_out.ptr, host_in.ptr, 128)) failed++;
+    }
+    samples[seq - 1] = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - start).count();
+  }
+  HIP_CHECK(hipStreamSynchronize(stream));
+  const double wall = std::chrono::duration<double>(std::chrono::steady_clock::now() - begin).count();
+  std::vector<unsigned long long> ticks(count, 0);
+  if (interactive) {
+    HIP_CHECK(hipMemcpy(ticks.data(), d_ticks.ptr, count * 8, hipMemcpyDeviceToHost));
+    int errors = 0;
+    HIP_CHECK(hipMemcpy(&errors, d_errors.ptr, 4, hipMemcpyDeviceToHost));
+    failed += (uint64_t)errors;
+  }
+  if (csv_path && *csv_path) {
+    FILE* f = std::fopen(csv_path, "w");
+    if (!f) throw Error(ST_ERR_INVALID, std::string("Cannot write ") + csv_path);
+    std::fprintf(f, "sequence,host_observation_us,device_round_trip_or_wait_us\n");
+    for (uint64_t i = 0; i < count; i++)
+      std::fprintf(f, "%llu,%.17g,%.17g\n", (unsigned long long)(i + 1), samples[i], ticks[i] * 1000.0 / wall_khz);
+    std::fclose(f);
+  }
+  std::vector<double> sorted = samples;
+  std::sort(sorted.begin(), sorted.end());
+  const double p50 = sorted[count / 2], p99 = sorted[std::min<size_t>(count - 1, (size_t)(count * 0.99))];
+  std::ostringstream o;
+  o.precision(17);
+  o << "{\"environment\": " << environment << ", \"mode\": \"" << mode << "\", \"events\": " << count
+    << ", \"failed\": " << failed << ", \"poll_policy\": \"" << (backoff ? "device-sleep-host-yield" : "tight")
+    << "\", \"wall_seconds\": " << wall << ", \"p50_us\": " << p50 << ", \"p99_us\": " << p99
+    << ", \"worst_us\": " << sorted.back() << ", \"boundary\": \""
+    << (mode == "gpu-ping" ? "host wait+ack service observation; device round trip in the CSV"
+                           : "host submission through the corresponding host-visible completion")
+    << "\"}";
+  if (failed) throw Error(ST_ERR_NUMERIC, "Transport checksum failure");
+  return o.str();
+}
+
+}  // namespace stamd
+
 static int write_string(const std::string& s, char* buffer, size_t cap, size_t* needed) {
   if (needed) *needed = s.size() + 1;
   if (buffer && cap) {
@@ -1273,6 +1475,14 @@ int st_runtime_trace_step(st_runtime* r, const float* input, char* names, size_t
       off += v.size();
     }
     write_string(o.str(), names, names_cap, names_needed);
+  });
+}
+
+int st_transport_bench(const char* mode, uint64_t count, int32_t backoff, const char* csv_path, char* report,
+                       size_t cap, size_t* needed) {
+  return guarded([&] {
+    if (!mode) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    write_string(stamd::transport_bench(mode, count, backoff != 0, csv_path), report, cap, needed);
   });
 }
 

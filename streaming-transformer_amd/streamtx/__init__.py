@@ -7,8 +7,8 @@ streamtx.build    hipcc build of libstamd.so for gfx950
 """
 from .model import (Checkpoint, ModelConfig, load_checkpoint, round_bf16, round_half, synthetic_checkpoint,
                     tensor_names, write_checkpoint)
-from .runtime import Backend, BatchRuntime, Runtime, RuntimeOptions, WeightStorage, library, probe
+from .runtime import Backend, BatchRuntime, Runtime, RuntimeOptions, WeightStorage, library, probe, transport_bench
 
 __all__ = ['Backend', 'BatchRuntime', 'Checkpoint', 'ModelConfig', 'Runtime', 'RuntimeOptions', 'WeightStorage', 'library',
-           'load_checkpoint', 'probe', 'round_bf16', 'round_half', 'synthetic_checkpoint', 'tensor_names',
+           'load_checkpoint', 'probe', 'transport_bench', 'round_bf16', 'round_half', 'synthetic_checkpoint', 'tensor_names',
            'write_checkpoint']

@@ -103,6 +103,8 @@ def library(path: os.PathLike | None = None) -> ctypes.CDLL:
                                           ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_runtime_info_json.argtypes = [P, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_probe_json.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+    lib.st_transport_bench.argtypes = [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_int32, ctypes.c_char_p,
+                                       ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_last_error.argtypes = []
     lib.st_last_error.restype = ctypes.c_char_p
     lib.st_batch_create.argtypes = [ctypes.POINTER(_Config), ctypes.c_int32, ctypes.POINTER(_Tensor),
@@ -118,7 +120,7 @@ def library(path: os.PathLike | None = None) -> ctypes.CDLL:
                  'st_runtime_snapshot', 'st_runtime_device_trace', 'st_runtime_device_run', 'st_runtime_phase_times',
                  'st_runtime_trace_step',
                  'st_runtime_info_json',
-                 'st_probe_json'):
+                 'st_probe_json', 'st_transport_bench'):
         getattr(lib, name).restype = ctypes.c_int
     _lib = lib
     return lib
@@ -163,6 +165,20 @@ def _marshal(config, tensors):
 def probe() -> dict:
     """Stream::probe() (src/cuda/Runtime.cu:134-161)."""
     return _json(library().st_probe_json)
+
+
+def transport_bench(mode: str, count: int, backoff: bool = False, output: str | None = None) -> dict:
+    """Stream::transportBench (include/Runtime.hpp:46): ping-pong, gpu-ping, empty,
+    empty-graph or copy; per-sample CSV to `output` when given."""
+    lib = library()
+    args = (mode.encode(), int(count), int(bool(backoff)), output.encode() if output else None)
+    needed = ctypes.c_size_t(0)
+    # One call runs the benchmark; the report is sized generously and re-read only if needed.
+    buf = ctypes.create_string_buffer(1 << 16)
+    _check(lib.st_transport_bench(*args, buf, len(buf), ctypes.byref(needed)))
+    if needed.value > len(buf):
+        raise RuntimeError('transport report exceeds 64 KiB')
+    return json.loads(buf.value.decode())
 
 
 class Runtime:

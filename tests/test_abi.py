@@ -73,3 +73,11 @@ def test_shape_mismatch_rejected_on_device_or_before():
     w['layers.0.q'] = np.zeros((64, 63), np.float32)
     with pytest.raises((RuntimeError, ValueError)):
         Runtime((c, w, False), RuntimeOptions(backend=Backend.FUSED))
+
+
+@pytest.mark.parametrize('mode,count,msg', [('bogus', 10, 'Unknown transport mode'), ('empty', 0, 'count')])
+def test_transport_bench_rejects_arguments(mode, count, msg):
+    # Validated before any device work (Stream::transportBench, include/Runtime.hpp:46).
+    from streamtx import transport_bench
+    with pytest.raises(RuntimeError, match=msg):
+        transport_bench(mode, count)
