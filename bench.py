@@ -13,7 +13,7 @@ already resident in HBM). The library synchronizes its stream before and after t
 launches. One JSON line is printed.
 
 Secondary measurements (skipped with --quick) go under "extra": host-service latency through
-step(), the device loop, the persistent worker, the transport floors (mailbox ping-pong, empty
+step(), scheduled arrivals at 2000 events/s, the device loop, the persistent worker, the transport floors (mailbox ping-pong, empty
 launch, empty graph, copy), the vendor GEMV baseline (rocBLAS projections
 in a captured graph) on the same workload, B independent streams over shared weights
 (Main, bfloat16 weights, W=128, B in 1, 16, 64, 256; --batched runs only that), and the Main
@@ -222,6 +222,13 @@ def main():
                 host.append((time.perf_counter() - s) * 1e6)
             extra['host_service_p50_us'] = nearest_rank(host, 0.5)
             extra['host_service_p99_us'] = nearest_rank(host, 0.99)
+            # Scheduled arrivals (the reference driver's scheduled mode): 2048 events offered at
+            # 2000 per second into a 4096-slot queue, latency from intended arrival to completion.
+            arrivals = rt.scheduled_run(events[fill:fill + 2048], rate=2000.0, queue=4096)['summary']
+            extra['scheduled_2000_per_s'] = {k: arrivals[k] for k in ('offered', 'completed', 'dropped')}
+            for k in ('arrival', 'service', 'queueing'):
+                extra['scheduled_2000_per_s'][k + '_p50_us'] = round(arrivals[k]['p50_us'], 1)
+                extra['scheduled_2000_per_s'][k + '_p99_us'] = round(arrivals[k]['p99_us'], 1)
             if backend == Backend.FUSED:
                 # Device loop inside one cooperative launch (the reference's deviceTrace).
                 n = c.window - 1 + 256

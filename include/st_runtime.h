@@ -167,6 +167,17 @@ int st_runtime_phase_times(st_runtime* runtime, const float* input, double* us, 
 int st_runtime_trace_step(st_runtime* runtime, const float* input, char* names, size_t names_cap,
                           size_t* names_needed, float* values, size_t values_cap, size_t* values_count);
 
+/* The scheduled-arrival mode of the reference's benchmark driver (bench/Main.cpp:282-342):
+ * a producer thread offers event i (inputs + i*features) at time i*1e9/rate ns after the
+ * schedule's start (bursty: in groups of 16 at the group's time) into a bounded queue of
+ * queue_capacity, dropping it when the queue is full; the calling thread runs st_runtime_step
+ * on each dequeued event in order. Every output holds `count` entries: the intended and
+ * enqueue times, the submit and completion times (ns since the schedule's start; NaN for a
+ * dropped event), the score (NaN when dropped) and the dropped flag. */
+int st_runtime_scheduled_run(st_runtime* runtime, const float* inputs, size_t count, double rate_per_second,
+                             size_t queue_capacity, int32_t bursty, double* intended_ns, double* enqueue_ns,
+                             double* submit_ns, double* complete_ns, float* scores, uint8_t* dropped);
+
 /* Json Runtime::info() const - src/cuda/Runtime.cu:570-594, as a JSON string. Writes at
  * most cap bytes (NUL-terminated) and the full length to *needed. */
 int st_runtime_info_json(st_runtime* runtime, char* buffer, size_t cap, size_t* needed);

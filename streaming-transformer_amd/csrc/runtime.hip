@@ -204,6 +204,11 @@ class Runtime {
   std::vector<std::pair<std::string, size_t>> trace_layout() const;
   std::vector<std::pair<std::string, std::vector<float>>> trace_step(const float* input);
   std::string info();
+  // Scheduled arrivals (bench/Main.cpp:282-342): a producer thread offers event i at its
+  // intended time into a bounded queue (dropping it when the queue is full); this thread
+  // steps the runtime on each dequeued event. Times in ns since the schedule's start.
+  void scheduled_run(const float* inputs, size_t count, double rate, size_t capacity, bool bursty, double* intended,
+                     double* enqueue, double* submit, double* complete, float* scores, uint8_t* dropped);
 
  private:
   void build_weights(const st_tensor* tensors, size_t count);
@@ -885,6 +890,72 @@ double Runtime::device_run(const float* inputs, size_t count, bool reset_first, 
   return total_ms * 1000.0 / count;
 }
 
+void Runtime::scheduled_run(const float* inputs, size_t count, double rate, size_t capacity, bool bursty,
+                            double* intended, double* enqueue, double* submit, double* complete, float* scores,
+                            uint8_t* dropped) {
+  if (!inputs || !intended || !enqueue || !submit || !complete || !scores || !dropped)
+    throw Error(ST_ERR_INVALID, "Null argument");
+  if (count == 0 || !(rate > 0) || !std::isfinite(rate) || capacity == 0)
+    throw Error(ST_ERR_INVALID, "Invalid rate, count or queue capacity");
+  using clock = std::chrono::steady_clock;
+  std::vector<size_t> queue(capacity);
+  std::atomic<size_t> head{0}, tail{0};
+  std::atomic<bool> done{false};
+  // The schedule starts 100 ms from now, so the producer is running before the first event.
+  const auto epoch = clock::now() + std::chrono::milliseconds(100);
+  auto ns_since = [&](clock::time_point t) { return std::chrono::duration<double, std::nano>(t - epoch).count(); };
+  std::exception_ptr producer_error;
+  std::thread producer([&] {
+    try {
+      for (size_t i = 0; i < count; i++) {
+        const double at = (double)(bursty ? (i / 16) * 16 : i) * 1e9 / rate;
+        intended[i] = at;
+        const auto when = epoch + std::chrono::nanoseconds((long long)at);
+        while (clock::now() < when) std::this_thread::yield();
+        enqueue[i] = ns_since(clock::now());
+        const size_t write = tail.load(std::memory_order_relaxed);
+        if (write - head.load(std::memory_order_acquire) == capacity) {
+          dropped[i] = 1;
+        } else {
+          dropped[i] = 0;
+          queue[write % capacity] = i;
+          tail.store(write + 1, std::memory_order_release);
+        }
+      }
+    } catch (...) {
+      producer_error = std::current_exception();
+    }
+    done.store(true, std::memory_order_release);
+  });
+  try {
+    while (true) {
+      const size_t read = head.load(std::memory_order_relaxed);
+      if (read == tail.load(std::memory_order_acquire)) {
+        // Re-read the tail after seeing `done`, so the last queued event is not lost.
+        if (done.load(std::memory_order_acquire) && read == tail.load(std::memory_order_acquire)) break;
+        std::this_thread::yield();
+        continue;
+      }
+      const size_t i = queue[read % capacity];
+      head.store(read + 1, std::memory_order_release);
+      submit[i] = ns_since(clock::now());
+      scores[i] = step(inputs + i * (size_t)c_.features);
+      complete[i] = ns_since(clock::now());
+    }
+  } catch (...) {
+    producer.join();
+    throw;
+  }
+  producer.join();
+  if (producer_error) std::rethrow_exception(producer_error);
+  for (size_t i = 0; i < count; i++) {
+    if (!dropped[i]) continue;
+    submit[i] = std::nan("");
+    complete[i] = std::nan("");
+    scores[i] = std::nanf("");
+  }
+}
+
 // Trace of one step (Runtime::traceStep, src/cuda/Runtime.cu:476-546), on the staged backend
 // like the reference. The step runs in the phase kernels, one launch at a time, so it leaves
 // exactly the state and score of an ordinary step; after each phase its output vector (x, q,
@@ -1483,6 +1554,16 @@ int st_transport_bench(const char* mode, uint64_t count, int32_t backoff, const 
   return guarded([&] {
     if (!mode) throw stamd::Error(ST_ERR_INVALID, "Null argument");
     write_string(stamd::transport_bench(mode, count, backoff != 0, csv_path), report, cap, needed);
+  });
+}
+
+int st_runtime_scheduled_run(st_runtime* r, const float* inputs, size_t count, double rate_per_second,
+                             size_t queue_capacity, int32_t bursty, double* intended_ns, double* enqueue_ns,
+                             double* submit_ns, double* complete_ns, float* scores, uint8_t* dropped) {
+  return guarded([&] {
+    if (!r) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    r->impl->scheduled_run(inputs, count, rate_per_second, queue_capacity, bursty != 0, intended_ns, enqueue_ns,
+                           submit_ns, complete_ns, scores, dropped);
   });
 }
 

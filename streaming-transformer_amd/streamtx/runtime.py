@@ -101,6 +101,8 @@ def library(path: os.PathLike | None = None) -> ctypes.CDLL:
     lib.st_runtime_phase_times.argtypes = [P, F, D, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_runtime_trace_step.argtypes = [P, F, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t), F,
                                           ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+    lib.st_runtime_scheduled_run.argtypes = [P, F, ctypes.c_size_t, ctypes.c_double, ctypes.c_size_t, ctypes.c_int32,
+                                             D, D, D, D, F, ctypes.POINTER(ctypes.c_uint8)]
     lib.st_runtime_info_json.argtypes = [P, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_probe_json.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_transport_bench.argtypes = [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_int32, ctypes.c_char_p,
@@ -118,7 +120,7 @@ def library(path: os.PathLike | None = None) -> ctypes.CDLL:
     for name in ('st_batch_create', 'st_batch_step', 'st_batch_reset', 'st_batch_snapshot', 'st_batch_device_run',
                  'st_runtime_create', 'st_runtime_step', 'st_runtime_reset', 'st_runtime_stop',
                  'st_runtime_snapshot', 'st_runtime_device_trace', 'st_runtime_device_run', 'st_runtime_phase_times',
-                 'st_runtime_trace_step',
+                 'st_runtime_trace_step', 'st_runtime_scheduled_run',
                  'st_runtime_info_json',
                  'st_probe_json', 'st_transport_bench'):
         getattr(lib, name).restype = ctypes.c_int
@@ -304,6 +306,38 @@ class Runtime:
         _check(lib.st_runtime_trace_step(self._handle(), _fptr(x), names, needed.value, ctypes.byref(needed),
                                          _fptr(values), total.value, ctypes.byref(total)))
         return {name: values[o:o + n].copy() for name, (o, n) in json.loads(names.value.decode()).items()}
+
+    def scheduled_run(self, events, rate: float, queue: int = 4096, bursty: bool = False) -> dict:
+        """Scheduled arrivals (bench/Main.cpp:282-342): arrays intended/enqueue/submit/complete
+        (ns), scores and dropped, plus the latency distributions of bench/analyze.py:32-52
+        (service = complete - submit, arrival = complete - intended, queueing = submit -
+        enqueue, injection = enqueue - intended; microseconds, nearest rank)."""
+        x = np.ascontiguousarray(events, dtype=np.float32).reshape(-1, self.config.features)
+        n = x.shape[0]
+        D = ctypes.POINTER(ctypes.c_double)
+        out = {k: np.empty(n, dtype=np.float64) for k in ('intended_ns', 'enqueue_ns', 'submit_ns', 'complete_ns')}
+        scores = np.empty(n, dtype=np.float32)
+        dropped = np.zeros(n, dtype=np.uint8)
+        _check(library().st_runtime_scheduled_run(
+            self._handle(), _fptr(x), n, float(rate), int(queue), int(bool(bursty)),
+            *(out[k].ctypes.data_as(D) for k in ('intended_ns', 'enqueue_ns', 'submit_ns', 'complete_ns')),
+            _fptr(scores), dropped.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8))))
+        kept = dropped == 0
+
+        def dist(v):
+            v = np.sort(np.asarray(v, dtype=np.float64))
+            if not len(v):
+                return {}
+            r = {name: float(v[int(np.ceil(q * len(v))) - 1]) for name, q in
+                 (('p50_us', .5), ('p95_us', .95), ('p99_us', .99), ('p999_us', .999))}
+            return dict(r, worst_us=float(v[-1]))
+
+        summary = dict(offered=n, completed=int(kept.sum()), dropped=int((~kept).sum()),
+                       service=dist((out['complete_ns'][kept] - out['submit_ns'][kept]) / 1e3),
+                       arrival=dist((out['complete_ns'][kept] - out['intended_ns'][kept]) / 1e3),
+                       queueing=dist((out['submit_ns'][kept] - out['enqueue_ns'][kept]) / 1e3),
+                       injection=dist((out['enqueue_ns'] - out['intended_ns']) / 1e3))
+        return dict(out, scores=scores, dropped=dropped.astype(bool), summary=summary)
 
     def info(self) -> dict:
         return _json(library().st_runtime_info_json, self._handle())

@@ -334,3 +334,33 @@ def test_trace_step_requires_staged_backend():
     with runtime((c, w, False), Backend.FUSED, 0) as rt:
         with pytest.raises(RuntimeError, match='staged'):
             rt.trace_step(np.zeros(c.features, dtype=np.float32))
+
+
+@pytest.mark.parametrize('backend', [Backend.FUSED, Backend.PERSISTENT])
+def test_scheduled_arrivals_step_every_kept_event_in_order(backend):
+    # bench/Main.cpp:282-342: offered events go through a bounded queue; the consumer steps
+    # the kept ones in order, so their scores equal plain stepping of the same subsequence.
+    c = SHAPES['small']
+    w = synthetic_checkpoint(c, seed=23)
+    events = _stream(c, 23, 400)
+    kw = dict(idle_seconds=10.0) if backend == Backend.PERSISTENT else {}
+    with runtime((c, w, False), backend, 0, **kw) as rt:
+        r = rt.scheduled_run(events, rate=4000.0, queue=4096)
+        s = r['summary']
+        assert s['offered'] == 400 and s['dropped'] == 0 and s['completed'] == 400
+        assert np.all(r['intended_ns'] <= r['enqueue_ns']) and np.all(r['enqueue_ns'] <= r['submit_ns'])
+        assert np.all(r['submit_ns'] < r['complete_ns'])
+        assert np.all(np.diff(r['submit_ns']) > 0)
+        assert s['service']['p50_us'] > 0 and s['arrival']['p50_us'] >= s['service']['p50_us']
+        rt.reset()
+        # A one-slot queue offered faster than service drops events; the kept ones still run in order.
+        r2 = rt.scheduled_run(events[:200], rate=1e6, queue=1)
+        kept = ~r2['dropped']
+        assert r2['summary']['dropped'] > 0 and kept.sum() == r2['summary']['completed'] > 0
+        assert np.all(np.isnan(r2['scores'][~kept]))
+    with runtime((c, w, False), Backend.FUSED, 0) as ref:
+        plain = np.array([ref.step(e) for e in events], dtype=np.float32)
+        np.testing.assert_array_equal(r['scores'], plain)
+        ref.reset()
+        plain2 = np.array([ref.step(e) for e in events[:200][kept]], dtype=np.float32)
+        np.testing.assert_array_equal(r2['scores'][kept], plain2)
