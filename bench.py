@@ -13,7 +13,7 @@ already resident in HBM). The library synchronizes its stream before and after t
 launches. One JSON line is printed.
 
 Secondary measurements (skipped with --quick) go under "extra": host-service latency through
-step(), scheduled arrivals at 2000 events/s, the device loop, the persistent worker, the transport floors (mailbox ping-pong, empty
+step(), scheduled arrivals at 2000 events/s, the same step in PyTorch-ROCm (eager and captured), the device loop, the persistent worker, the transport floors (mailbox ping-pong, empty
 launch, empty graph, copy), the vendor GEMV baseline (rocBLAS projections
 in a captured graph) on the same workload, B independent streams over shared weights
 (Main, bfloat16 weights, W=128, B in 1, 16, 64, 256; --batched runs only that), and the Main
@@ -83,6 +83,109 @@ def batched_streams(counts=(1, 16, 64, 256), steps=64):
                         'events_per_s': round(b / (p50 * 1e-6)), 'algorithmic_bytes_per_step': step_bytes,
                         'achieved_gbs': round(gbs, 1), 'hbm_frac': round(gbs / HBM_PEAK_GBS, 4)}
     return out
+
+
+def torch_baseline(c: ModelConfig, weights, events, fill: int, steps: int = 128):
+    """The same single-stream step written with PyTorch-ROCm operators in FP32 (the
+    reference's bench/torch_bench.py comparison): eager, and captured once in a hipGraph with
+    the position held on the device (ring slot, valid-window mask and RoPE angles computed from
+    it). Returns p50 microseconds per step for both and the largest score difference from this
+    build's runtime on the same events (a sanity check, not a parity bar)."""
+    import torch
+
+    dev = torch.device('cuda')
+    T = {k: torch.from_numpy(np.ascontiguousarray(v, dtype=np.float32)).to(dev) for k, v in weights.items()}
+    L, d, H, W, dh = c.layers, c.width, c.heads, c.window, c.dim
+    keys = torch.zeros(L, H, W, dh, device=dev)
+    values = torch.zeros_like(keys)
+    pos = torch.zeros((), dtype=torch.int64, device=dev)
+    inv = torch.pow(torch.tensor(10000.0, device=dev), -torch.arange(0, dh, 2, device=dev, dtype=torch.float32) / dh)
+    slots = torch.arange(W, device=dev)
+    event = torch.zeros(c.features, device=dev)
+    score = torch.zeros(1, device=dev)
+
+    def rms(x, g):
+        return x * torch.rsqrt(x.pow(2).mean() + c.epsilon) * g
+
+    def rope(v, cos, sin):
+        v = v.view(H, dh // 2, 2)
+        a, b = v[..., 0], v[..., 1]
+        return torch.stack((a * cos - b * sin, a * sin + b * cos), -1).reshape(d)
+
+    def step():
+        ang = pos.to(torch.float32) * inv
+        cos, sin = torch.cos(ang), torch.sin(ang)
+        slot = torch.remainder(pos, W).view(1)
+        mask = (slots <= pos).view(1, 1, W)
+        x = T['input'] @ event
+        for l in range(L):
+            p = f'layers.{l}.'
+            n = rms(x, T[p + 'norm1'])
+            q = rope(T[p + 'q'] @ n, cos, sin)
+            k = rope(T[p + 'k'] @ n, cos, sin)
+            v = T[p + 'v'] @ n
+            keys[l].index_copy_(1, slot, k.view(H, 1, dh))
+            values[l].index_copy_(1, slot, v.view(H, 1, dh))
+            logits = torch.matmul(keys[l], q.view(H, dh, 1)).view(H, 1, W) / (dh ** 0.5)
+            prob = torch.softmax(logits.masked_fill(~mask, float('-inf')), -1)
+            attn = torch.matmul(prob, values[l]).reshape(d)
+            x = x + T[p + 'out'] @ attn
+            n = rms(x, T[p + 'norm2'])
+            g = T[p + 'gate'] @ n
+            x = x + T[p + 'down'] @ (torch.nn.functional.silu(g) * (T[p + 'up'] @ n))
+        score.copy_(T['score'] @ rms(x, T['final_norm']))
+        pos.add_(1)
+
+    timed_events = torch.from_numpy(np.ascontiguousarray(events[fill:fill + steps])).to(dev)
+
+    def timed(run, n):
+        start = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+        start[0].record()
+        for i in range(n):
+            event.copy_(timed_events[i])  # device-to-device: inputs resident, like the runtime's timing
+            run()
+            start[i + 1].record()
+        torch.cuda.synchronize()
+        return np.array([start[i].elapsed_time(start[i + 1]) * 1e3 for i in range(n)])
+
+    with torch.no_grad():
+        for i in range(fill):  # fill the window
+            event.copy_(torch.from_numpy(events[i]).to(dev))
+            step()
+        state = (keys.clone(), values.clone(), pos.clone())  # the filled window
+        eager = timed(step, steps)
+        eager_scores = []
+        # Graph capture of the same step on a side stream, then replays checked against eager.
+        keys.copy_(state[0]), values.copy_(state[1]), pos.copy_(state[2])
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        keys.copy_(state[0]), values.copy_(state[1]), pos.copy_(state[2])
+        with torch.cuda.graph(graph):
+            step()
+        keys.copy_(state[0]), values.copy_(state[1]), pos.copy_(state[2])
+        for i in range(8):
+            event.copy_(torch.from_numpy(events[fill + i]).to(dev))
+            step()
+            eager_scores.append(float(score))
+        keys.copy_(state[0]), values.copy_(state[1]), pos.copy_(state[2])
+        replay_diff = 0.0
+        for i in range(8):
+            event.copy_(torch.from_numpy(events[fill + i]).to(dev))
+            graph.replay()
+            torch.cuda.synchronize()
+            replay_diff = max(replay_diff, abs(float(score) - eager_scores[i]))
+        graphed = timed(graph.replay, steps)
+    with Runtime((c, weights, False), RuntimeOptions(backend=Backend.FUSED, blocks=0)) as rt:
+        rt.device_run(events[:fill], reset=True)
+        ours = [rt.step(e) for e in events[fill:fill + 8]]
+    diff = max(abs(a - b) for a, b in zip(ours, eager_scores))
+    return {'eager_p50_us': round(float(np.median(eager)), 1), 'graph_p50_us': round(float(np.median(graphed)), 1),
+            'graph_replay_vs_eager_max_abs': replay_diff, 'score_max_abs_diff_vs_runtime': diff,
+            'torch': torch.__version__}
 
 
 def window_sweep(windows=(32, 64, 128, 256, 512), steps=2048):
@@ -255,6 +358,11 @@ def main():
             rt.device_run(events[:fill], reset=True)
             _, vper = rt.device_run(events[fill:fill + min(args.steps, 256)])
         extra['vendor_gemv_graph_p50_us'] = nearest_rank(vper, 0.5)
+    if not args.quick and args.precision == 'fp32':
+        try:
+            extra['torch_baseline'] = torch_baseline(c, weights, events, fill)
+        except Exception as e:  # torch on the GPU box is a third-party baseline, not the product
+            extra['torch_baseline'] = {'error': f'{type(e).__name__}: {e}'[:300]}
     if not args.quick:
         # Transport floors under a step (the reference's transportBench modes).
         extra['transport_p50_us'] = {m: round(transport_bench(m, 2000)['p50_us'], 2)
