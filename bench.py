@@ -179,7 +179,9 @@ def torch_baseline(c: ModelConfig, weights, events, fill: int, steps: int = 128)
             torch.cuda.synchronize()
             replay_diff = max(replay_diff, abs(float(score) - eager_scores[i]))
         graphed = timed(graph.replay, steps)
-    with Runtime((c, weights, False), RuntimeOptions(backend=Backend.FUSED, blocks=0)) as rt:
+    # The staged backend (bit-identical to the fused one) needs no cooperative launch, which a
+    # second process on the GPU may not get while the first holds the cooperative queue.
+    with Runtime((c, weights, False), RuntimeOptions(backend=Backend.CUDA, blocks=0)) as rt:
         rt.device_run(events[:fill], reset=True)
         ours = [rt.step(e) for e in events[fill:fill + 8]]
     diff = max(abs(a - b) for a, b in zip(ours, eager_scores))
@@ -276,11 +278,20 @@ def main():
     ap.add_argument('--backend', choices=['fused', 'graph', 'cuda'], default='fused')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--quick', action='store_true', help='skip the secondary measurements')
+    ap.add_argument('--torch-baseline', action='store_true',
+                    help='only the PyTorch comparison (FP32, eager and captured); bench.py runs it as a child')
     ap.add_argument('--batched', action='store_true',
                     help='only the batched-streams measurement (B in 1, 16, 64, 256; --steps timed steps each)')
     ap.add_argument('--copy-calibration', type=int, metavar='MIB', default=0,
                     help='only run 8 plain device copies of MIB MiB (reference kernel for HBM counters)')
     args = ap.parse_args()
+    if args.torch_baseline:
+        c, seed = CONFIGS[args.config]
+        weights = synthetic_checkpoint(c, seed=seed)
+        fill = c.window - 1 + args.warmup
+        events = np.random.default_rng([seed, 1]).standard_normal((fill + 128, c.features), dtype=np.float32)
+        print(json.dumps(torch_baseline(c, weights, events, fill)), flush=True)
+        return
     if args.batched:
         print(json.dumps(batched_streams(steps=args.steps)), flush=True)
         return
@@ -325,9 +336,9 @@ def main():
                 host.append((time.perf_counter() - s) * 1e6)
             extra['host_service_p50_us'] = nearest_rank(host, 0.5)
             extra['host_service_p99_us'] = nearest_rank(host, 0.99)
-            # Scheduled arrivals (the reference driver's scheduled mode): 2048 events offered at
-            # 2000 per second into a 4096-slot queue, latency from intended arrival to completion.
-            arrivals = rt.scheduled_run(events[fill:fill + 2048], rate=2000.0, queue=4096)['summary']
+            # Scheduled arrivals (the reference driver's scheduled mode): the timed events offered
+            # at 2000 per second into a 4096-slot queue, latency from intended arrival to completion.
+            arrivals = rt.scheduled_run(events[fill:fill + args.steps], rate=2000.0, queue=4096)['summary']
             extra['scheduled_2000_per_s'] = {k: arrivals[k] for k in ('offered', 'completed', 'dropped')}
             for k in ('arrival', 'service', 'queueing'):
                 extra['scheduled_2000_per_s'][k + '_p50_us'] = round(arrivals[k]['p50_us'], 1)
@@ -359,10 +370,18 @@ def main():
             _, vper = rt.device_run(events[fill:fill + min(args.steps, 256)])
         extra['vendor_gemv_graph_p50_us'] = nearest_rank(vper, 0.5)
     if not args.quick and args.precision == 'fp32':
+        # torch brings its own HIP runtime, which does not start in a process where this
+        # library's runtime already runs: the comparison runs in a child process.
+        import subprocess
+        cmd = [sys.executable, str(Path(__file__).resolve()), '--torch-baseline', '--config', args.config,
+               '--warmup', str(args.warmup)]
         try:
-            extra['torch_baseline'] = torch_baseline(c, weights, events, fill)
-        except Exception as e:  # torch on the GPU box is a third-party baseline, not the product
-            extra['torch_baseline'] = {'error': f'{type(e).__name__}: {e}'[:300]}
+            proc = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+            lines = [ln for ln in proc.stdout.splitlines() if ln.startswith('{')]
+            extra['torch_baseline'] = json.loads(lines[-1]) if proc.returncode == 0 and lines else \
+                {'error': (proc.stderr or proc.stdout)[-300:]}
+        except subprocess.TimeoutExpired:
+            extra['torch_baseline'] = {'error': 'timeout'}
     if not args.quick:
         # Transport floors under a step (the reference's transportBench modes).
         extra['transport_p50_us'] = {m: round(transport_bench(m, 2000)['p50_us'], 2)
