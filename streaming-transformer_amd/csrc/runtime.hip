@@ -900,18 +900,18 @@ void Runtime::scheduled_run(const float* inputs, size_t count, double rate, size
   using clock = std::chrono::steady_clock;
   std::vector<size_t> queue(capacity);
   std::atomic<size_t> head{0}, tail{0};
-  std::atomic<bool> done{false};
+  std::atomic<bool> done{false}, cancel{false};
   // The schedule starts 100 ms from now, so the producer is running before the first event.
   const auto epoch = clock::now() + std::chrono::milliseconds(100);
   auto ns_since = [&](clock::time_point t) { return std::chrono::duration<double, std::nano>(t - epoch).count(); };
   std::exception_ptr producer_error;
   std::thread producer([&] {
     try {
-      for (size_t i = 0; i < count; i++) {
+      for (size_t i = 0; i < count && !cancel.load(std::memory_order_relaxed); i++) {
         const double at = (double)(bursty ? (i / 16) * 16 : i) * 1e9 / rate;
         intended[i] = at;
         const auto when = epoch + std::chrono::nanoseconds((long long)at);
-        while (clock::now() < when) std::this_thread::yield();
+        while (clock::now() < when && !cancel.load(std::memory_order_relaxed)) std::this_thread::yield();
         enqueue[i] = ns_since(clock::now());
         const size_t write = tail.load(std::memory_order_relaxed);
         if (write - head.load(std::memory_order_acquire) == capacity) {
@@ -943,6 +943,7 @@ void Runtime::scheduled_run(const float* inputs, size_t count, double rate, size
       complete[i] = ns_since(clock::now());
     }
   } catch (...) {
+    cancel.store(true, std::memory_order_relaxed);  // a failed step ends the schedule early
     producer.join();
     throw;
   }
@@ -1292,19 +1293,8 @@ std::string transport_bench(const std::string& mode, uint64_t count, bool backof
   int device = 0, wall_khz = 100000;
   HIP_CHECK(hipGetDevice(&device));
   HIP_CHECK(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, device));
-  hipStream_t stream;
-  HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
-  struct StreamGuard {
-    hipStream_t s;
-    hipGraph_t g = nullptr;
-    hipGraphExec_t e = nullptr;
-    ~StreamGuard() {
-      (void)hipStreamSynchronize(s);
-      if (e) (void)hipGraphExecDestroy(e);
-      if (g) (void)hipGraphDestroy(g);
-      (void)hipStreamDestroy(s);
-    }
-  } guard{stream};
+  // Buffers first: the stream guard below is destroyed before them, so a kernel still
+  // running when an error unwinds is joined before its memory is freed.
   MappedBuffer box_buf, in_buf;
   box_buf.alloc(sizeof(PingBox));
   in_buf.alloc(32 * 4);
@@ -1320,6 +1310,19 @@ std::string transport_bench(const std::string& mode, uint64_t count, bool backof
   d_errors.alloc(4);
   HIP_CHECK(hipMemset(d_errors.ptr, 0, 4));
   HIP_CHECK(hipMemset(d_ticks.ptr, 0, count * 8));
+  hipStream_t stream;
+  HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+  struct StreamGuard {
+    hipStream_t s;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t e = nullptr;
+    ~StreamGuard() {
+      (void)hipStreamSynchronize(s);
+      if (e) (void)hipGraphExecDestroy(e);
+      if (g) (void)hipGraphDestroy(g);
+      (void)hipStreamDestroy(s);
+    }
+  } guard{stream};
   if (mode == "empty-graph") {
     HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
     hipLaunchKernelGGL(transport_empty_kernel, dim3(1), dim3(1), 0, stream);
