@@ -13,7 +13,7 @@ already resident in HBM). The library synchronizes its stream before and after t
 launches. One JSON line is printed.
 
 Secondary measurements (skipped with --quick) go under "extra": host-service latency through
-step(), scheduled arrivals at 2000 events/s, the same step in PyTorch-ROCm (eager and captured), the device loop, the persistent worker, the transport floors (mailbox ping-pong, empty
+step(), Large in the mixed and bfloat16-weight modes, scheduled arrivals at 2000 events/s, the same step in PyTorch-ROCm (eager and captured), the device loop, the persistent worker, the transport floors (mailbox ping-pong, empty
 launch, empty graph, copy), the vendor GEMV baseline (rocBLAS projections
 in a captured graph) on the same workload, B independent streams over shared weights
 (Main, bfloat16 weights, W=128, B in 1, 16, 64, 256; --batched runs only that), and the Main
@@ -382,6 +382,23 @@ def main():
                 {'error': (proc.stderr or proc.stdout)[-300:]}
         except subprocess.TimeoutExpired:
             extra['torch_baseline'] = {'error': 'timeout'}
+    if not args.quick and args.config == 'large' and args.precision == 'fp32':
+        # The same Large workload in the other storage modes: mixed (FP16 weights and K/V, the
+        # reference's cast points) and bfloat16 weights with FP32 K/V.
+        extra['other_precisions'] = {}
+        for prec in ('mixed', 'bf16w'):
+            pm = prec == 'mixed'
+            pw = synthetic_checkpoint(c, seed=seed, mixed=pm)
+            popts = RuntimeOptions(backend=Backend.FUSED, blocks=0,
+                                   weight_dtype=WeightStorage.BF16 if prec == 'bf16w' else WeightStorage.AS_MODEL)
+            with Runtime((c, pw, pm), popts) as rt:
+                rt.device_run(events[:fill], reset=True)
+                pmean, pper = rt.device_run(events[fill:fill + min(args.steps, 512)])
+            pbytes = weight_bytes_per_step(c, 2) + kv_bytes_per_step(c, 2 if pm else 4, c.window)
+            extra['other_precisions'][prec] = {
+                'p50_us': round(nearest_rank(pper, 0.5), 2), 'p99_us': round(nearest_rank(pper, 0.99), 2),
+                'algorithmic_bytes_per_step': pbytes,
+                'roofline_frac': round(pbytes / (pmean * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     if not args.quick:
         # Transport floors under a step (the reference's transportBench modes).
         extra['transport_p50_us'] = {m: round(transport_bench(m, 2000)['p50_us'], 2)
