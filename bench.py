@@ -62,22 +62,24 @@ def kv_bytes_per_step(c: ModelConfig, kvb: int, valid: int) -> int:
     return 2 * c.layers * c.width * valid * kvb + 2 * c.layers * c.width * kvb
 
 
-def batched_streams(counts=(1, 16, 64, 256), steps=64):
-    """B independent streams over shared weights (st_batch_*): Main architecture with bfloat16
-    weights, W=128, as in the batched configuration. Each B runs a full window of events
+def batched_streams(counts=(1, 16, 64, 256), steps=64, mode='bf16w'):
+    """B independent streams over shared weights (st_batch_*): Main architecture, W=128, as in
+    the batched configuration, with bfloat16 weights and FP32 K/V (mode 'bf16w') or the
+    reference's mixed mode (FP16 weights and K/V). Each B runs a full window of events
     (untimed), then `steps` timed steps with a HIP event after each. Algorithmic bytes per
-    step: the weights once plus every stream's K/V window and new rows (FP32)."""
+    step: the weights once plus every stream's K/V window and new rows."""
     c, seed = CONFIGS['main']
-    weights = synthetic_checkpoint(c, seed=seed)
-    out = {'workload': f'main bf16w batched streams, W={c.window}', 'steps': steps}
+    mixed = mode == 'mixed'
+    weights = synthetic_checkpoint(c, seed=seed, mixed=mixed)
+    out = {'workload': f'main {mode} batched streams, W={c.window}', 'steps': steps}
     for b in counts:
         rng = np.random.default_rng([seed, 2, b])
         events = rng.standard_normal((c.window + steps, b, c.features), dtype=np.float32)
-        with BatchRuntime((c, weights, False), b, WeightStorage.BF16) as rt:
+        with BatchRuntime((c, weights, mixed), b, WeightStorage.AS_MODEL if mixed else WeightStorage.BF16) as rt:
             rt.device_run(events[:c.window])
             mean, per = rt.device_run(events[c.window:])
         p50 = nearest_rank(per, 0.5)
-        step_bytes = weight_bytes_per_step(c, 2) + b * kv_bytes_per_step(c, 4, c.window)
+        step_bytes = weight_bytes_per_step(c, 2) + b * kv_bytes_per_step(c, 2 if mixed else 4, c.window)
         gbs = step_bytes / (mean * 1e-6) / 1e9
         out[f'B{b}'] = {'p50_us_per_step': round(p50, 2), 'mean_us_per_step': round(mean, 2),
                         'events_per_s': round(b / (p50 * 1e-6)), 'algorithmic_bytes_per_step': step_bytes,
@@ -293,7 +295,8 @@ def main():
         print(json.dumps(torch_baseline(c, weights, events, fill)), flush=True)
         return
     if args.batched:
-        print(json.dumps(batched_streams(steps=args.steps)), flush=True)
+        print(json.dumps({'bf16w': batched_streams(steps=args.steps),
+                          'mixed': batched_streams(steps=args.steps, mode='mixed')}), flush=True)
         return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
@@ -404,6 +407,7 @@ def main():
         extra['transport_p50_us'] = {m: round(transport_bench(m, 2000)['p50_us'], 2)
                                      for m in ('ping-pong', 'gpu-ping', 'empty', 'empty-graph', 'copy')}
         extra['batched'] = batched_streams()
+        extra['batched_mixed'] = batched_streams(mode='mixed')
         extra['window_sweep'] = window_sweep()
 
     achieved = bytes_step / (mean_us * 1e-6) / 1e9

@@ -198,9 +198,10 @@ int st_probe_json(char* buffer, size_t cap, size_t* needed);
 
 /* Extension (no counterpart in the reference, which is single-stream by design,
  * docs/Architecture.md:3): `streams` independent streams (1..256) sharing one set of
- * weights, each with its own K/V ring, hidden state and position. FP32 checkpoints only
- * (mixed must be 0); weight_dtype as in st_options. A step advances every stream by one
- * event; the projections run as MFMA GEMMs over the streams. */
+ * weights, each with its own K/V ring, hidden state and position. FP32 checkpoints with FP32
+ * or bfloat16 weight storage (weight_dtype as in st_options), or mixed checkpoints (FP16
+ * weights and K/V, the reference's cast points). A step advances every stream by one event;
+ * the projections run as MFMA GEMMs over the streams. */
 typedef struct st_batch st_batch;
 int st_batch_create(const st_config* config, int32_t mixed, const st_tensor* tensors, size_t tensor_count,
                     int32_t streams, int32_t weight_dtype, st_batch** out);

@@ -1,11 +1,15 @@
 // Batched independent streams on gfx950: B streams share the weights and each keeps its own
 // K/V ring, hidden state and position. One step advances every stream by one event. The
-// projections become skinny GEMMs [B x K] . W^T computed with MFMA (v_mfma_f32_16x16x4_f32:
-// FP32 operands, FP32 accumulation; bfloat16 weights are widened exactly), split over K
-// across the waves of a workgroup and summed in LDS in a fixed order, with the RMSNorm in the
-// prologue and the phase's epilogue (RoPE and ring write, residual, SwiGLU) fused. Activations,
-// K/V and reductions are FP32, so each stream follows the single-stream runtime's arithmetic
-// up to summation order.
+// projections become skinny GEMMs [B x K] . W^T on MFMA, split over K across the waves of a
+// workgroup and summed in LDS in a fixed order, with the phase's epilogue (RoPE and ring write,
+// residual, SwiGLU) fused. Storage modes:
+//  - FP32 and bfloat16 weights: FP32 activations, K/V and reductions; RMSNorm folded into the
+//    projection prologue;
+//  - mixed (the reference's FP16 mode): FP16 weights and K/V ring, every value rounded to FP16
+//    at the reference's cast points, so each GEMM input is exactly FP16 and runs on
+//    v_mfma_f32_16x16x32_f16 with FP32 accumulation; the norms are materialized (their output
+//    is cast before the projection).
+// Each stream follows the single-stream runtime's arithmetic up to summation order.
 #pragma once
 
 #include "step_device.hpp"
@@ -17,6 +21,7 @@ constexpr int kBatchTile = 16;   // MFMA rows
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 struct BatchArgs {
   int streams, streams_p;  // B and the padded batch (16, 32 or a multiple of 64)
@@ -27,12 +32,13 @@ struct BatchArgs {
   uint32_t w_input, w_final_norm, w_score;
   LayerWeights layer[kMaxLayers];
   const float* rope_freq;          // [dim / 2]
-  float* keys;                     // [B][L][H][W][dh]
-  float* values;
+  void* keys;                      // [B][L][H][W][dh], FP32 (FP16 in mixed mode)
+  void* values;
   float* hidden;                   // [B][L][d]
   unsigned long long* position;    // [B]
   float* in;                       // [Bp][features_p] events
   float* x;                        // [Bp][width_p] residual stream
+  float* xn;                       // [Bp][width_p] normalized x (mixed mode)
   float* attn;                     // [Bp][width_p] attention output
   float* act;                      // [Bp][ffn_p] SwiGLU output
   float* q;                        // [Bp][width] rotated queries
@@ -110,16 +116,28 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
 #pragma unroll
       for (int c = 0; c < CT; c++) acc[i][t][c] = f4v{0.f, 0.f, 0.f, 0.f};
     }
-  if constexpr (P == kFp32) {
+  static_assert(!(kNorm && P == kMixed), "mixed mode materializes its norms");
+  if constexpr (P == kFp32 || (P == kMixed && E == kEpInput)) {
+    // FP32 MFMA. Mixed mode takes this path for the input projection only: its operand is
+    // the raw FP32 event, and its FP16 weights widen exactly.
     const float* xr = X + (size_t)(t0 * kBatchTile + r16) * ldx + 4 * g;
-    const float* wr = reinterpret_cast<const float*>(a.weights + woff) + (size_t)(n0 + r16) * ldw + 4 * g;
+    const char* wr = a.weights + woff + ((size_t)(n0 + r16) * ldw + 4 * g) * (P == kFp32 ? 4 : 2);
     const float* gr = reinterpret_cast<const float*>(a.weights + w_norm) + 4 * g;
     struct Frag {
       float4 w[CT], gn, x[NT];
     };
     auto load = [&](int k, Frag& f) {
 #pragma unroll
-      for (int c = 0; c < CT; c++) f.w[c] = *reinterpret_cast<const float4*>(wr + (size_t)c * kBatchTile * ldw + k);
+      for (int c = 0; c < CT; c++) {
+        if constexpr (P == kFp32) {
+          f.w[c] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(wr) + (size_t)c * kBatchTile * ldw + k);
+        } else {
+          const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(wr) +
+                                                          (size_t)c * kBatchTile * ldw + k);
+          f.w[c] = make_float4(half_to_float((unsigned short)(h.x & 0xffffu)), half_to_float((unsigned short)(h.x >> 16)),
+                               half_to_float((unsigned short)(h.y & 0xffffu)), half_to_float((unsigned short)(h.y >> 16)));
+        }
+      }
       // The norm vector holds `width` values (a multiple of 16): a group of 4 is all in or out.
       f.gn = make_float4(0.f, 0.f, 0.f, 0.f);
       if constexpr (kNorm)
@@ -171,7 +189,7 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
         for (int i = 0; i < SW; i++) mma(i, f[i]);
       }
     }
-  } else {
+  } else if constexpr (P == kBf16w) {
     const float* xr = X + (size_t)(t0 * kBatchTile + r16) * ldx + 8 * g;
     const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.weights + woff) + (size_t)(n0 + r16) * ldw + 8 * g;
     const uint16_t* gr = reinterpret_cast<const uint16_t*>(a.weights + w_norm) + 8 * g;
@@ -245,6 +263,55 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
         for (int i = 0; i < SW; i++) mma(i, f[i]);
       }
     }
+  } else {
+    // Mixed mode: the operand holds FP16 values (cast points), the weights are FP16; one
+    // v_mfma_f32_16x16x32_f16 per 32-k block, lane (r16, g) holding k = kb + 8 g .. + 7.
+    const float* xr = X + (size_t)(t0 * kBatchTile + r16) * ldx + 8 * g;
+    const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.weights + woff) + (size_t)(n0 + r16) * ldw + 8 * g;
+    struct Frag {
+      uint4 w[CT];
+      float4 xlo[NT], xhi[NT];
+    };
+    auto load = [&](int k, Frag& f) {
+#pragma unroll
+      for (int c = 0; c < CT; c++) f.w[c] = *reinterpret_cast<const uint4*>(wr + (size_t)c * kBatchTile * ldw + k);
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const float* p = xr + (size_t)t * kBatchTile * ldx + k;
+        f.xlo[t] = *reinterpret_cast<const float4*>(p);
+        f.xhi[t] = *reinterpret_cast<const float4*>(p + 4);
+      }
+    };
+    auto mma = [&](int i, const Frag& f) {
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const f16x8 xh = {(_Float16)f.xlo[t].x, (_Float16)f.xlo[t].y, (_Float16)f.xlo[t].z, (_Float16)f.xlo[t].w,
+                          (_Float16)f.xhi[t].x, (_Float16)f.xhi[t].y, (_Float16)f.xhi[t].z, (_Float16)f.xhi[t].w};
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+          acc[i][t][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, __builtin_bit_cast(f16x8, f.w[c]), acc[i][t][c], 0,
+                                                                0, 0);
+      }
+    };
+    if constexpr (SW == 1) {
+      const int k0 = wave * slice;
+      Frag cur;
+      load(k0, cur);
+      for (int kk = 0; kk < slice; kk += 32) {
+        Frag nxt;
+        load(k0 + (kk + 32 < slice ? kk + 32 : kk), nxt);
+        mma(0, cur);
+        cur = nxt;
+      }
+    } else {
+      for (int kk = 0; kk < slice; kk += 32) {
+        Frag f[SW];
+#pragma unroll
+        for (int i = 0; i < SW; i++) load((wave * SW + i) * slice + kk, f[i]);
+#pragma unroll
+        for (int i = 0; i < SW; i++) mma(i, f[i]);
+      }
+    }
   }
   // A wave holding two slices adds them here: the first level of the tree.
 #pragma unroll
@@ -288,6 +355,10 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
       s0 *= scale;
       s1 *= scale;
     }
+    // Projection outputs are cast (mixed mode), then each epilogue casts where the reference
+    // does (src/cuda/Primitives.cuh:148-239); cast<P> is the identity for FP32 storage.
+    s0 = cast<P>(s0);
+    s1 = cast<P>(s1);
     const int n = n0 + cc;
     float* xb = a.x + (size_t)b * a.width_p;
     if constexpr (E == kEpInput) {
@@ -303,8 +374,8 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
         const float angle = (float)pos * a.rope_freq[e >> 1];
         const float co = cosf(angle), si = sinf(angle);
         const float ra = va * co - vb * si, rb = va * si + vb * co;
-        va = ra;
-        vb = rb;
+        va = cast<P>(ra);
+        vb = cast<P>(rb);
       }
       if (sec == 0) {
         a.q[(size_t)b * a.width + i] = va;
@@ -313,32 +384,51 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
         const int h = i / a.dim, d = i - h * a.dim;
         const int slot = (int)(pos % (unsigned long long)a.window);
         const size_t ring = ((((size_t)b * a.layers + layer) * a.heads + h) * a.window + slot) * a.dim + d;
-        float* dst = sec == 1 ? a.keys : a.values;
-        dst[ring] = va;
-        dst[ring + 1] = vb;
+        void* dst = sec == 1 ? a.keys : a.values;
+        if constexpr (P == kMixed) {
+          reinterpret_cast<uint16_t*>(dst)[ring] = float_to_half(va);
+          reinterpret_cast<uint16_t*>(dst)[ring + 1] = float_to_half(vb);
+        } else {
+          reinterpret_cast<float*>(dst)[ring] = va;
+          reinterpret_cast<float*>(dst)[ring + 1] = vb;
+        }
       }
     } else if constexpr (E == kEpOut) {
-      xb[n] = xb[n] + s0;
+      xb[n] = cast<P>(xb[n] + s0);
     } else if constexpr (E == kEpGateUp) {
-      a.act[(size_t)b * a.ffn_p + (n >> 1)] = (s0 / (1.0f + expf(-s0))) * s1;
+      a.act[(size_t)b * a.ffn_p + (n >> 1)] = cast<P>((s0 / (1.0f + expf(-s0))) * s1);
     } else {
-      const float v = xb[n] + s0;
+      const float v = cast<P>(xb[n] + s0);
       xb[n] = v;
       a.hidden[((size_t)b * a.layers + layer) * a.width + n] = v;
     }
   }
 }
 
+// Four consecutive ring elements of K or V (FP32, or FP16 in mixed mode) as floats.
+template <int P>
+__device__ __forceinline__ float4 ring4(const void* ring, size_t i) {
+  if constexpr (P == kMixed) {
+    const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(ring) + i);
+    return make_float4(half_to_float((unsigned short)(h.x & 0xffffu)), half_to_float((unsigned short)(h.x >> 16)),
+                       half_to_float((unsigned short)(h.y & 0xffffu)), half_to_float((unsigned short)(h.y >> 16)));
+  } else {
+    return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(ring) + i);
+  }
+}
+
 // Attention of one (stream, head) over the stream's valid ring slots [0, valid)
-// (src/cuda/Primitives.cuh:167-219): logits q.K/sqrt(dh), softmax, weighted V. Slot order does
-// not change the result beyond summation order. Four waves; every load is a coalesced row:
-//  - logits: 16 lanes per K row (16 bytes each, rows of up to 64 FP32 per pass), a 16-lane
-//    DPP sum, so a wave covers 4 rows per load;
+// (src/cuda/Primitives.cuh:167-219): logits q.K/sqrt(dh), softmax, weighted V, cast. Slot order
+// does not change the result beyond summation order. Four waves; every load is a coalesced
+// row:
+//  - logits: 16 lanes per K row (4 elements each, rows of up to 64 elements per pass), a
+//    16-lane DPP sum, so a wave covers 4 rows per load;
 //  - softmax: workgroup max and sum through LDS;
-//  - values: lane group (slot s mod 16) accumulates its slots' V rows, 16 bytes per lane, and
-//    the 16 groups are summed in LDS in group order.
+//  - values: lane group (slot s mod 16) accumulates its slots' V rows, 4 elements per lane,
+//    and the 16 groups are summed in LDS in group order.
 // Needs dh a multiple of 4; dynamic LDS holds `window` floats of probabilities.
 constexpr int kAttnThreads = 256;
+template <int P>
 __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs* __restrict__ ap, int layer) {
   const BatchArgs& a = *ap;
   extern __shared__ float pr[];
@@ -350,8 +440,6 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
   const unsigned long long t = a.position[b];
   const int valid = t + 1 < (unsigned long long)a.window ? (int)(t + 1) : a.window;
   const size_t base = (((size_t)b * a.layers + layer) * a.heads + h) * (size_t)a.window * dim;
-  const float* K = a.keys + base;
-  const float* V = a.values + base;
   const float* q = a.q + (size_t)b * a.width + h * dim;
   const float div = sqrtf((float)dim);
   float mx = -INFINITY;
@@ -360,10 +448,10 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
 #pragma unroll 4
   for (int s0 = 0; s0 < valid; s0 += kAttnThreads / 16) {
     const int s = s0 + grp;
-    const float* kr = K + (size_t)(s < valid ? s : valid - 1) * dim;
+    const size_t row = base + (size_t)(s < valid ? s : valid - 1) * dim;
     float dot = 0.f;
     for (int d = 4 * r; d < dim; d += 64) {
-      const float4 kv = *reinterpret_cast<const float4*>(kr + d);
+      const float4 kv = ring4<P>(a.keys, row + d);
       const float4 qv = *reinterpret_cast<const float4*>(q + d);
       dot += qv.x * kv.x;
       dot += qv.y * kv.y;
@@ -400,7 +488,7 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
 #pragma unroll 4
       for (int s = grp; s < valid; s += 16) {
         const float p = pr[s];
-        const float4 vv = *reinterpret_cast<const float4*>(V + (size_t)s * dim + d);
+        const float4 vv = ring4<P>(a.values, base + (size_t)s * dim + d);
         o.x += p * vv.x;
         o.y += p * vv.y;
         o.z += p * vv.z;
@@ -419,17 +507,48 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
         acc.w += v.w;
       }
       float* od = out + d0 + 4 * tid;
-      od[0] = acc.x / sum;
-      od[1] = acc.y / sum;
-      od[2] = acc.z / sum;
-      od[3] = acc.w / sum;
+      od[0] = cast<P>(acc.x / sum);
+      od[1] = cast<P>(acc.y / sum);
+      od[2] = cast<P>(acc.z / sum);
+      od[3] = cast<P>(acc.w / sum);
     }
     __syncthreads();
   }
 }
 
-// Final RMSNorm and score of every stream (src/cuda/Runtime.cu:380-383), then the position
-// advance. One wave per stream.
+// One element of a norm or score vector in the arena, decoded to FP32.
+template <int P>
+__device__ __forceinline__ float batch_weight(const char* w, uint32_t off, int i) {
+  if constexpr (P == kFp32) return reinterpret_cast<const float*>(w + off)[i];
+  if constexpr (P == kMixed) return half_to_float(reinterpret_cast<const uint16_t*>(w + off)[i]);
+  return bf16_to_float(reinterpret_cast<const uint16_t*>(w + off)[i]);
+}
+
+// Mixed mode: RMSNorm of every stream's x into xn with the output cast to FP16
+// (src/cuda/Primitives.cuh:122-135); padding columns and padding streams are zero. One
+// workgroup of 256 threads per row of the padded batch.
+__global__ __launch_bounds__(256) void batch_norm_mixed(const BatchArgs* __restrict__ ap, uint32_t w_norm) {
+  const BatchArgs& a = *ap;
+  __shared__ float red[4];
+  const int b = blockIdx.x;
+  const float* xb = a.x + (size_t)b * a.width_p;
+  float* out = a.xn + (size_t)b * a.width_p;
+  if (b >= a.streams) {
+    for (int i = threadIdx.x; i < a.width_p; i += blockDim.x) out[i] = 0.f;
+    return;
+  }
+  float s = 0.f;
+  for (int i = threadIdx.x; i < a.width; i += blockDim.x) s += xb[i] * xb[i];
+  s = wave_total(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  const float scale = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)a.width + a.epsilon);
+  for (int i = threadIdx.x; i < a.width_p; i += blockDim.x)
+    out[i] = i < a.width ? cast<kMixed>(xb[i] * scale * batch_weight<kMixed>(a.weights, w_norm, i)) : 0.f;
+}
+
+// Final RMSNorm (cast in mixed mode) and score of every stream (src/cuda/Runtime.cu:380-383;
+// the score itself is not cast), then the position advance. One wave per stream.
 template <int P>
 __global__ __launch_bounds__(64) void batch_final(const BatchArgs* __restrict__ ap) {
   const BatchArgs& a = *ap;
@@ -440,15 +559,8 @@ __global__ __launch_bounds__(64) void batch_final(const BatchArgs* __restrict__ 
   const float scale = 1.0f / sqrtf(wave_total(s) / (float)a.width + a.epsilon);
   float acc = 0.f;
   for (int i = lane; i < a.width; i += 64) {
-    float wn, ws;
-    if constexpr (P == kFp32) {
-      wn = reinterpret_cast<const float*>(a.weights + a.w_final_norm)[i];
-      ws = reinterpret_cast<const float*>(a.weights + a.w_score)[i];
-    } else {
-      wn = __builtin_bit_cast(float, (unsigned)reinterpret_cast<const unsigned short*>(a.weights + a.w_final_norm)[i] << 16);
-      ws = __builtin_bit_cast(float, (unsigned)reinterpret_cast<const unsigned short*>(a.weights + a.w_score)[i] << 16);
-    }
-    acc += ws * (xb[i] * scale * wn);
+    const float wn = batch_weight<P>(a.weights, a.w_final_norm, i), ws = batch_weight<P>(a.weights, a.w_score, i);
+    acc += ws * cast<P>(xb[i] * scale * wn);
   }
   acc = wave_total(acc);
   if (lane == 0) {
@@ -458,14 +570,16 @@ __global__ __launch_bounds__(64) void batch_final(const BatchArgs* __restrict__ 
 }
 
 // Zero the state of stream `stream` (every stream when negative): K/V rows, hidden, position.
-__global__ void batch_reset(const BatchArgs* __restrict__ ap, int stream) {
+// `kv_words` is the size of one stream's K (or V) ring in 4-byte words.
+__global__ void batch_reset(const BatchArgs* __restrict__ ap, int stream, size_t kv_words) {
   const BatchArgs& a = *ap;
   const int b0 = stream < 0 ? 0 : stream, b1 = stream < 0 ? a.streams : stream + 1;
-  const size_t per = (size_t)a.layers * a.heads * a.window * a.dim;
   const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x, step = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)b0 * per + tid; i < (size_t)b1 * per; i += step) {
-    a.keys[i] = 0.f;
-    a.values[i] = 0.f;
+  unsigned* k = reinterpret_cast<unsigned*>(a.keys);
+  unsigned* v = reinterpret_cast<unsigned*>(a.values);
+  for (size_t i = (size_t)b0 * kv_words + tid; i < (size_t)b1 * kv_words; i += step) {
+    k[i] = 0u;
+    v[i] = 0u;
   }
   const size_t hper = (size_t)a.layers * a.width;
   for (size_t i = (size_t)b0 * hper + tid; i < (size_t)b1 * hper; i += step) a.hidden[i] = 0.f;

@@ -7,7 +7,7 @@
 
 class Batch {
  public:
-  Batch(const st_config& config, const st_tensor* tensors, size_t count, int streams, int weight_dtype);
+  Batch(const st_config& config, bool mixed, const st_tensor* tensors, size_t count, int streams, int weight_dtype);
   ~Batch();
   void step(const float* inputs, float* scores);
   void reset(int stream);
@@ -20,8 +20,10 @@ class Batch {
   void project(const float* X, int ld, uint32_t woff, int N, uint32_t norm, int layer);
   int group_tiles(int cols) const;
   bool wide_qkv_ = false, wide_gateup_ = false;  // two column tiles per workgroup
+  size_t kv_words_ = 0;                           // one stream's K (or V) ring in 4-byte words
   void launch() {
     if (prec_ == kFp32) launch_sequence<kFp32>();
+    else if (prec_ == kMixed) launch_sequence<kMixed>();
     else launch_sequence<kBf16w>();
   }
   void sync() { HIP_CHECK(hipStreamSynchronize(stream_)); }
@@ -31,14 +33,15 @@ class Batch {
   hipStream_t stream_ = nullptr;
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;
-  DeviceBuffer weights_, keys_, values_, hidden_, position_, in_, x_, attn_, act_, q_, score_, rope_, args_dev_;
+  DeviceBuffer weights_, keys_, values_, hidden_, position_, in_, x_, xn_, attn_, act_, q_, score_, rope_, args_dev_;
   PinnedBuffer host_in_, host_out_;
   StepArgs offsets_{};  // weight arena offsets (shared layout with the single-stream runtime)
   BatchArgs args_{};
   const BatchArgs* dargs_ = nullptr;
 };
 
-Batch::Batch(const st_config& config, const st_tensor* tensors, size_t count, int streams, int weight_dtype)
+Batch::Batch(const st_config& config, bool mixed, const st_tensor* tensors, size_t count, int streams,
+             int weight_dtype)
     : c_(config) {
   validate_config(c_);
   if (streams < 1 || streams > kBatchMax)
@@ -47,7 +50,9 @@ Batch::Batch(const st_config& config, const st_tensor* tensors, size_t count, in
     throw Error(ST_ERR_INVALID, "Unknown weight storage");
   if (c_.width % kBatchTile || (2 * c_.ffn) % kBatchTile)
     throw Error(ST_ERR_INVALID, "Batched streams need width and 2*ffn to be multiples of 16");
-  prec_ = weight_dtype == ST_WEIGHTS_BF16 ? kBf16w : kFp32;
+  if (mixed && weight_dtype == ST_WEIGHTS_BF16)
+    throw Error(ST_ERR_INVALID, "bfloat16 weight storage applies to FP32 checkpoints only");
+  prec_ = mixed ? kMixed : weight_dtype == ST_WEIGHTS_BF16 ? kBf16w : kFp32;
   streams_ = streams;
   // Padded batch: 16 or 32 rows, else a multiple of 64, so that every projection's batch
   // groups (1, 2 or 4 tiles of 16) divide it.
@@ -97,20 +102,22 @@ Batch::Batch(const st_config& config, const st_tensor* tensors, size_t count, in
   HIP_CHECK(hipMemcpy(rope_.ptr, freq.data(), freq.size() * 4, hipMemcpyHostToDevice));
   a.rope_freq = reinterpret_cast<const float*>(rope_.ptr);
 
-  const size_t ring = (size_t)streams_ * c_.layers * c_.width * c_.window;
   auto zeroed = [&](DeviceBuffer& buf, size_t floats) {
     buf.alloc(floats * 4);
     HIP_CHECK(hipMemset(buf.ptr, 0, std::max<size_t>(floats * 4, 256)));
     return reinterpret_cast<float*>(buf.ptr);
   };
-  a.keys = zeroed(keys_, ring);
-  a.values = zeroed(values_, ring);
+  // K/V rings: FP32, or FP16 in mixed mode (kv_words_ 4-byte words per stream and ring).
+  kv_words_ = (size_t)c_.layers * c_.width * c_.window * (prec_ == kMixed ? 2 : 4) / 4;
+  a.keys = zeroed(keys_, (size_t)streams_ * kv_words_);
+  a.values = zeroed(values_, (size_t)streams_ * kv_words_);
   a.hidden = zeroed(hidden_, (size_t)streams_ * c_.layers * c_.width);
   position_.alloc((size_t)streams_ * 8);
   HIP_CHECK(hipMemset(position_.ptr, 0, (size_t)streams_ * 8));
   a.position = reinterpret_cast<unsigned long long*>(position_.ptr);
   a.in = zeroed(in_, (size_t)streams_p_ * a.features_p);
   a.x = zeroed(x_, (size_t)streams_p_ * a.width_p);
+  a.xn = zeroed(xn_, (size_t)streams_p_ * a.width_p);
   a.attn = zeroed(attn_, (size_t)streams_p_ * a.width_p);
   a.act = zeroed(act_, (size_t)streams_p_ * a.ffn_p);
   a.q = zeroed(q_, (size_t)streams_p_ * a.width);
@@ -173,16 +180,26 @@ template <int P>
 void Batch::launch_sequence() {
   const BatchArgs& a = args_;
   const int d = c_.width, F = c_.ffn;
+  // Mixed mode casts each norm's output, so its norms run first into xn; the other modes fold
+  // the norm into the projection (kNorm).
+  constexpr bool kFold = P != kMixed;
+  const float* nx = kFold ? a.x : a.xn;
+  auto norm = [&](uint32_t w_norm) {
+    if constexpr (!kFold)
+      hipLaunchKernelGGL(batch_norm_mixed, dim3(streams_p_), dim3(256), 0, stream_, dargs_, w_norm);
+  };
   project<P, kEpInput, false, 1, 1>(a.in, a.features_p, a.w_input, d, 0u, 0);
   for (int l = 0; l < c_.layers; l++) {
     const LayerWeights& w = a.layer[l];
-    if (wide_qkv_) project<P, kEpQkv, true, 2, 2>(a.x, a.width_p, w.qkv, 3 * d, w.norm1, l);
-    else project<P, kEpQkv, true, 1, 1>(a.x, a.width_p, w.qkv, 3 * d, w.norm1, l);
-    hipLaunchKernelGGL(batch_attention, dim3(streams_ * c_.heads), dim3(kAttnThreads), (size_t)c_.window * 4, stream_,
-                       dargs_, l);
+    norm(w.norm1);
+    if (wide_qkv_) project<P, kEpQkv, kFold, 2, 2>(nx, a.width_p, w.qkv, 3 * d, w.norm1, l);
+    else project<P, kEpQkv, kFold, 1, 1>(nx, a.width_p, w.qkv, 3 * d, w.norm1, l);
+    hipLaunchKernelGGL(batch_attention<P>, dim3(streams_ * c_.heads), dim3(kAttnThreads), (size_t)c_.window * 4,
+                       stream_, dargs_, l);
     project<P, kEpOut, false, 1, 1>(a.attn, a.width_p, w.out, d, 0u, l);
-    if (wide_gateup_) project<P, kEpGateUp, true, 2, 2>(a.x, a.width_p, w.gateup, 2 * F, w.norm2, l);
-    else project<P, kEpGateUp, true, 1, 1>(a.x, a.width_p, w.gateup, 2 * F, w.norm2, l);
+    norm(w.norm2);
+    if (wide_gateup_) project<P, kEpGateUp, kFold, 2, 2>(nx, a.width_p, w.gateup, 2 * F, w.norm2, l);
+    else project<P, kEpGateUp, kFold, 1, 1>(nx, a.width_p, w.gateup, 2 * F, w.norm2, l);
     project<P, kEpDown, false, 1, 1>(a.act, a.ffn_p, w.down, d, 0u, l);
   }
   hipLaunchKernelGGL(batch_final<P>, dim3(streams_), dim3(64), 0, stream_, dargs_);
@@ -203,7 +220,7 @@ void Batch::step(const float* inputs, float* scores) {
 
 void Batch::reset(int stream) {
   if (stream < -1 || stream >= streams_) throw Error(ST_ERR_INVALID, "Stream index out of range");
-  hipLaunchKernelGGL(batch_reset, dim3(256), dim3(256), 0, stream_, dargs_, stream);
+  hipLaunchKernelGGL(batch_reset, dim3(256), dim3(256), 0, stream_, dargs_, stream, kv_words_);
   HIP_CHECK(hipGetLastError());
   sync();
 }
@@ -214,8 +231,19 @@ void Batch::snapshot(int stream, uint64_t* position, float* keys, float* values,
   const size_t ring = (size_t)c_.layers * c_.width * c_.window;
   if (position)
     HIP_CHECK(hipMemcpy(position, args_.position + stream, 8, hipMemcpyDeviceToHost));
-  if (keys) HIP_CHECK(hipMemcpy(keys, args_.keys + (size_t)stream * ring, ring * 4, hipMemcpyDeviceToHost));
-  if (values) HIP_CHECK(hipMemcpy(values, args_.values + (size_t)stream * ring, ring * 4, hipMemcpyDeviceToHost));
+  auto download = [&](const void* base, float* dst) {
+    if (!dst) return;
+    const char* src = reinterpret_cast<const char*>(base) + (size_t)stream * kv_words_ * 4;
+    if (prec_ == kMixed) {
+      std::vector<uint16_t> h(ring);
+      HIP_CHECK(hipMemcpy(h.data(), src, ring * 2, hipMemcpyDeviceToHost));
+      for (size_t i = 0; i < ring; i++) dst[i] = host_half_to_float(h[i]);
+    } else {
+      HIP_CHECK(hipMemcpy(dst, src, ring * 4, hipMemcpyDeviceToHost));
+    }
+  };
+  download(args_.keys, keys);
+  download(args_.values, values);
   if (hidden)
     HIP_CHECK(hipMemcpy(hidden, args_.hidden + (size_t)stream * c_.layers * c_.width, (size_t)c_.layers * c_.width * 4,
                         hipMemcpyDeviceToHost));

@@ -1592,9 +1592,8 @@ int st_batch_create(const st_config* config, int32_t mixed, const st_tensor* ten
   return guarded([&] {
     if (!config || !tensors || !out) throw stamd::Error(ST_ERR_INVALID, "Null argument");
     *out = nullptr;
-    if (mixed) throw stamd::Error(ST_ERR_INVALID, "Batched streams take FP32 checkpoints (FP32 or bfloat16 weights)");
     auto r = std::make_unique<st_batch>();
-    r->impl = std::make_unique<stamd::Batch>(*config, tensors, count, streams, weight_dtype);
+    r->impl = std::make_unique<stamd::Batch>(*config, mixed != 0, tensors, count, streams, weight_dtype);
     *out = r.release();
   });
 }

@@ -88,23 +88,54 @@ def test_bf16_weights_match_oracle_on_rounded_weights():
             _check_state(rt.snapshot(b), oracles[b].snapshot())
 
 
-@pytest.mark.parametrize('weight_dtype', [WeightStorage.AS_MODEL, WeightStorage.BF16])
-def test_stream_independent_of_batch(weight_dtype):
+@pytest.mark.parametrize('weight_dtype,mixed', [(WeightStorage.AS_MODEL, False), (WeightStorage.BF16, False),
+                                                (WeightStorage.AS_MODEL, True)])
+def test_stream_independent_of_batch(weight_dtype, mixed):
     c = SHAPES['small']
-    w = synthetic_checkpoint(c, seed=13)
+    w = synthetic_checkpoint(c, seed=13, mixed=mixed)
     steps, streams = 70, 40
     events = _events(c, 13, steps, streams)
-    with batch((c, w, False), streams, weight_dtype) as rt:
+    with batch((c, w, mixed), streams, weight_dtype) as rt:
         many = np.stack([rt.step(events[i]) for i in range(steps)])
         states = [rt.snapshot(b) for b in (0, 21, 39)]
     for b, state in zip((0, 21, 39), states):
-        with batch((c, w, False), 1, weight_dtype) as one:
+        with batch((c, w, mixed), 1, weight_dtype) as one:
             alone = np.array([one.step(events[i, b:b + 1])[0] for i in range(steps)], dtype=np.float32)
             np.testing.assert_array_equal(alone, many[:, b])
             ref = one.snapshot(0)
         assert ref[0] == state[0]
         for x, y in zip(ref[1:], state[1:]):
             np.testing.assert_array_equal(x, y)
+
+
+@pytest.mark.parametrize('name,streams,steps', [('main', 16, 40), ('small', 19, 90)])
+def test_mixed_streams_meet_the_reference_policy(name, streams, steps):
+    # Mixed mode: FP16 weights and K/V with the reference's cast points; each stream against
+    # the mixed oracle under the reference's numerical policy v3 (include/Numerical.hpp).
+    c = SHAPES[name]
+    w = synthetic_checkpoint(c, seed=16, mixed=True)
+    events = _events(c, 16, steps, streams)
+    oracles = [Oracle(c, w, mixed=True, threads=8) for _ in range(streams)]
+    scores = np.empty((steps, streams), dtype=np.float32)
+    refs = np.empty_like(scores)
+    with batch((c, w, True), streams) as rt:
+        for i in range(steps):
+            if i == steps // 2:
+                rt.reset(3)
+                oracles[3].reset()
+            scores[i] = rt.step(events[i])
+            refs[i] = [o.step(events[i, b]) for b, o in enumerate(oracles)]
+        for b in range(streams):
+            pos, k, v, h = rt.snapshot(b)
+            opos, ok, ov, oh = oracles[b].snapshot()
+            assert pos == opos
+            for a in (k, v, h):
+                assert np.array_equal(a, a.astype(np.float16).astype(np.float32))
+            res = numerical.mixed_state_passes(k, v, h, ok, ov, oh)
+            assert res['passed'], (b, res['failures'][:2])
+    for b in range(streams):
+        res = numerical.score_errors(scores[:, b], refs[:, b], c.layers)
+        assert res['passed'], (b, res)
 
 
 def test_reset_one_and_all_and_device_run_equals_stepping():
@@ -150,8 +181,8 @@ def test_invalid_arguments_are_rejected():
     for streams in (0, 257):
         with pytest.raises(RuntimeError, match='Streams'):
             BatchRuntime((c, w, False), streams)
-    with pytest.raises(RuntimeError, match='FP32'):
-        BatchRuntime((c, synthetic_checkpoint(c, seed=15, mixed=True), True), 4)
+    with pytest.raises(RuntimeError, match='bfloat16'):
+        BatchRuntime((c, synthetic_checkpoint(c, seed=15, mixed=True), True), 4, WeightStorage.BF16)
     odd = ModelConfig(1, 40, 1, 40, 8, 40)
     with pytest.raises(RuntimeError, match='multiples of 16'):
         BatchRuntime((odd, synthetic_checkpoint(odd, seed=15), False), 4)
