@@ -254,8 +254,10 @@ void Batch::snapshot(int stream, uint64_t* position, float* keys, float* values,
 // copy of that step's inputs, with a HIP event after each. Returns the mean microseconds per
 // step and, when per_step is not NULL, each step's event-to-event duration.
 double Batch::device_run(const float* inputs, size_t count, double* per_step) {
-  if (!inputs || count == 0 || count > (1u << 20)) throw Error(ST_ERR_INVALID, "Invalid trace");
   const int fp = args_.features_p;
+  // The padded copy is staged on the host and the device: at most 4 GiB.
+  if (!inputs || count == 0 || count > ((size_t)1 << 30) / ((size_t)streams_p_ * fp))
+    throw Error(ST_ERR_INVALID, "Invalid trace (empty, or more than 4 GiB of padded inputs)");
   std::vector<float> padded(count * (size_t)streams_p_ * fp, 0.f);
   for (size_t i = 0; i < count; i++)
     for (int b = 0; b < streams_; b++)

@@ -798,9 +798,10 @@ void Runtime::launch_trace_t(const float* events, int count, unsigned long long*
 double Runtime::device_trace(const float* inputs, size_t count, double* per_event) {
   if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
   if (persistent()) throw Error(ST_ERR_INVALID, "Device traces run on launch-per-step backends, not the persistent worker");
-  if (!inputs || count == 0 || count > (size_t)std::numeric_limits<int>::max())
-    throw Error(ST_ERR_INVALID, "Invalid trace");
   const int fp = args_.features_p;
+  // The padded copy is staged on the host and the device: at most 4 GiB.
+  if (!inputs || count == 0 || count > ((size_t)1 << 30) / (size_t)fp)
+    throw Error(ST_ERR_INVALID, "Invalid trace (empty, or more than 4 GiB of padded inputs)");
   std::vector<float> padded(count * (size_t)fp, 0.f);
   for (size_t i = 0; i < count; i++)
     std::memcpy(&padded[i * fp], inputs + i * c_.features, (size_t)c_.features * 4);
@@ -853,9 +854,10 @@ double Runtime::device_trace(const float* inputs, size_t count, double* per_even
 double Runtime::device_run(const float* inputs, size_t count, bool reset_first, double* per_event) {
   if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
   if (persistent()) throw Error(ST_ERR_INVALID, "Device runs use launch-per-step backends, not the persistent worker");
-  if (!inputs || count == 0 || count > (size_t)std::numeric_limits<int>::max())
-    throw Error(ST_ERR_INVALID, "Invalid trace");
   const int fp = args_.features_p;
+  // The padded copy is staged on the host and the device: at most 4 GiB.
+  if (!inputs || count == 0 || count > ((size_t)1 << 30) / (size_t)fp)
+    throw Error(ST_ERR_INVALID, "Invalid trace (empty, or more than 4 GiB of padded inputs)");
   std::vector<float> padded(count * (size_t)fp, 0.f);
   for (size_t i = 0; i < count; i++)
     std::memcpy(&padded[i * fp], inputs + i * c_.features, (size_t)c_.features * 4);
