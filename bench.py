@@ -277,7 +277,7 @@ def main():
     ap.add_argument('--warmup', type=int, default=64)
     ap.add_argument('--config', choices=sorted(CONFIGS), default='large')
     ap.add_argument('--precision', choices=['fp32', 'bf16w', 'mixed'], default='fp32')
-    ap.add_argument('--backend', choices=['fused', 'graph', 'cuda'], default='fused')
+    ap.add_argument('--backend', choices=['fused', 'graph', 'cuda', 'cublas', 'cublas-graph'], default='fused')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--quick', action='store_true', help='skip the secondary measurements')
     ap.add_argument('--torch-baseline', action='store_true',
@@ -312,7 +312,8 @@ def main():
     fill = c.window - 1 + args.warmup
     rng = np.random.default_rng([seed, 1])  # input stream distinct from the weight stream
     events = rng.standard_normal((fill + args.steps, c.features), dtype=np.float32)
-    backend = {'fused': Backend.FUSED, 'graph': Backend.GRAPH, 'cuda': Backend.CUDA}[args.backend]
+    backend = {'fused': Backend.FUSED, 'graph': Backend.GRAPH, 'cuda': Backend.CUDA, 'cublas': Backend.CUBLAS,
+               'cublas-graph': Backend.CUBLAS_GRAPH}[args.backend]
     opts = RuntimeOptions(backend=backend, blocks=0,
                           weight_dtype=WeightStorage.BF16 if args.precision == 'bf16w' else WeightStorage.AS_MODEL)
     wb = 4 if args.precision == 'fp32' else 2
@@ -415,7 +416,8 @@ def main():
                 'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None,
                 'algorithmic_bytes_per_step': bytes_step,
                 'roofline_us_per_step': bytes_step / (HBM_PEAK_GBS * 1e9) * 1e6,
-                'kernel': 'fused_kernel' if backend == Backend.FUSED else 'phase_kernel sequence'}
+                'kernel': {Backend.FUSED: 'fused_kernel', Backend.CUBLAS: 'rocBLAS gemv + stage kernels',
+                           Backend.CUBLAS_GRAPH: 'rocBLAS gemv + stage kernels'}.get(backend, 'phase_kernel sequence')}
     roofline['traffic'] = traffic_per_launch(
         ROOT / 'profiles' / f'traffic_{args.backend}_kernel_{args.config}_{args.precision}.md')
     roofline['frac_p50'] = round(bytes_step / (p50 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
