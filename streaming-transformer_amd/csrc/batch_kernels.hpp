@@ -38,9 +38,9 @@ struct BatchArgs {
   unsigned long long* position;    // [B]
   float* in;                       // [Bp][features_p] events
   float* x;                        // [Bp][width_p] residual stream
-  float* xn;                       // [Bp][width_p] normalized x (mixed mode)
-  float* attn;                     // [Bp][width_p] attention output
-  float* act;                      // [Bp][ffn_p] SwiGLU output
+  float* xn;                       // [Bp][width_p] normalized x (mixed mode, FP16)
+  float* attn;                     // [Bp][width_p] attention output (FP16 in mixed mode)
+  float* act;                      // [Bp][ffn_p] SwiGLU output (FP16 in mixed mode)
   float* q;                        // [Bp][width] rotated queries
   float* score;                    // [B]
 };
@@ -95,7 +95,7 @@ __device__ __forceinline__ void split3(const float (&x)[8], unsigned (&ph)[4], u
 // 1 / sqrt(sum / d + eps).
 template <int P, int E, bool kNorm, int NT, int CT, int SW>
 __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs* __restrict__ ap,
-                                                               const float* __restrict__ X, int ldx, uint32_t woff,
+                                                               const void* __restrict__ X, int ldx, uint32_t woff,
                                                                int ldw, int N, int K, uint32_t w_norm, int layer) {
   constexpr int kWaves = kSlices / SW;
   const BatchArgs& a = *ap;
@@ -120,7 +120,7 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
   if constexpr (P == kFp32 || (P == kMixed && E == kEpInput)) {
     // FP32 MFMA. Mixed mode takes this path for the input projection only: its operand is
     // the raw FP32 event, and its FP16 weights widen exactly.
-    const float* xr = X + (size_t)(t0 * kBatchTile + r16) * ldx + 4 * g;
+    const float* xr = reinterpret_cast<const float*>(X) + (size_t)(t0 * kBatchTile + r16) * ldx + 4 * g;
     const char* wr = a.weights + woff + ((size_t)(n0 + r16) * ldw + 4 * g) * (P == kFp32 ? 4 : 2);
     const float* gr = reinterpret_cast<const float*>(a.weights + w_norm) + 4 * g;
     struct Frag {
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
       }
     }
   } else if constexpr (P == kBf16w) {
-    const float* xr = X + (size_t)(t0 * kBatchTile + r16) * ldx + 8 * g;
+    const float* xr = reinterpret_cast<const float*>(X) + (size_t)(t0 * kBatchTile + r16) * ldx + 8 * g;
     const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.weights + woff) + (size_t)(n0 + r16) * ldw + 8 * g;
     const uint16_t* gr = reinterpret_cast<const uint16_t*>(a.weights + w_norm) + 8 * g;
     struct Frag {
@@ -264,34 +264,27 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
       }
     }
   } else {
-    // Mixed mode: the operand holds FP16 values (cast points), the weights are FP16; one
-    // v_mfma_f32_16x16x32_f16 per 32-k block, lane (r16, g) holding k = kb + 8 g .. + 7.
-    const float* xr = X + (size_t)(t0 * kBatchTile + r16) * ldx + 8 * g;
+    // Mixed mode: the operand is an FP16 buffer (its values are cast points) and the weights
+    // are FP16; one v_mfma_f32_16x16x32_f16 per 32-k block, lane (r16, g) holding
+    // k = kb + 8 g .. + 7 of both, 16 bytes each.
+    const uint16_t* xr = reinterpret_cast<const uint16_t*>(X) + (size_t)(t0 * kBatchTile + r16) * ldx + 8 * g;
     const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.weights + woff) + (size_t)(n0 + r16) * ldw + 8 * g;
     struct Frag {
-      uint4 w[CT];
-      float4 xlo[NT], xhi[NT];
+      uint4 w[CT], x[NT];
     };
     auto load = [&](int k, Frag& f) {
 #pragma unroll
       for (int c = 0; c < CT; c++) f.w[c] = *reinterpret_cast<const uint4*>(wr + (size_t)c * kBatchTile * ldw + k);
 #pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const float* p = xr + (size_t)t * kBatchTile * ldx + k;
-        f.xlo[t] = *reinterpret_cast<const float4*>(p);
-        f.xhi[t] = *reinterpret_cast<const float4*>(p + 4);
-      }
+      for (int t = 0; t < NT; t++) f.x[t] = *reinterpret_cast<const uint4*>(xr + (size_t)t * kBatchTile * ldx + k);
     };
     auto mma = [&](int i, const Frag& f) {
 #pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const f16x8 xh = {(_Float16)f.xlo[t].x, (_Float16)f.xlo[t].y, (_Float16)f.xlo[t].z, (_Float16)f.xlo[t].w,
-                          (_Float16)f.xhi[t].x, (_Float16)f.xhi[t].y, (_Float16)f.xhi[t].z, (_Float16)f.xhi[t].w};
+      for (int t = 0; t < NT; t++)
 #pragma unroll
         for (int c = 0; c < CT; c++)
-          acc[i][t][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, __builtin_bit_cast(f16x8, f.w[c]), acc[i][t][c], 0,
-                                                                0, 0);
-      }
+          acc[i][t][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, f.x[t]),
+                                                                __builtin_bit_cast(f16x8, f.w[c]), acc[i][t][c], 0, 0, 0);
     };
     if constexpr (SW == 1) {
       const int k0 = wave * slice;
@@ -396,7 +389,9 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
     } else if constexpr (E == kEpOut) {
       xb[n] = cast<P>(xb[n] + s0);
     } else if constexpr (E == kEpGateUp) {
-      a.act[(size_t)b * a.ffn_p + (n >> 1)] = cast<P>((s0 / (1.0f + expf(-s0))) * s1);
+      const float v = cast<P>((s0 / (1.0f + expf(-s0))) * s1);
+      if constexpr (P == kMixed) reinterpret_cast<uint16_t*>(a.act)[(size_t)b * a.ffn_p + (n >> 1)] = float_to_half(v);
+      else a.act[(size_t)b * a.ffn_p + (n >> 1)] = v;
     } else {
       const float v = cast<P>(xb[n] + s0);
       xb[n] = v;
@@ -480,7 +475,6 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
   if (lane == 0) wred[wave] = sum;
   __syncthreads();
   sum = (wred[0] + wred[1]) + (wred[2] + wred[3]);
-  float* out = a.attn + (size_t)b * a.width_p + h * dim;
   for (int d0 = 0; d0 < dim; d0 += 64) {
     const int d = d0 + 4 * r;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -506,11 +500,13 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
         acc.z += v.z;
         acc.w += v.w;
       }
-      float* od = out + d0 + 4 * tid;
-      od[0] = cast<P>(acc.x / sum);
-      od[1] = cast<P>(acc.y / sum);
-      od[2] = cast<P>(acc.z / sum);
-      od[3] = cast<P>(acc.w / sum);
+      const float o4[4] = {acc.x / sum, acc.y / sum, acc.z / sum, acc.w / sum};
+      const size_t oi = (size_t)b * a.width_p + h * dim + d0 + 4 * tid;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        if constexpr (P == kMixed) reinterpret_cast<uint16_t*>(a.attn)[oi + j] = float_to_half(o4[j]);
+        else a.attn[oi + j] = o4[j];
+      }
     }
     __syncthreads();
   }
@@ -532,9 +528,9 @@ __global__ __launch_bounds__(256) void batch_norm_mixed(const BatchArgs* __restr
   __shared__ float red[4];
   const int b = blockIdx.x;
   const float* xb = a.x + (size_t)b * a.width_p;
-  float* out = a.xn + (size_t)b * a.width_p;
+  uint16_t* out = reinterpret_cast<uint16_t*>(a.xn) + (size_t)b * a.width_p;
   if (b >= a.streams) {
-    for (int i = threadIdx.x; i < a.width_p; i += blockDim.x) out[i] = 0.f;
+    for (int i = threadIdx.x; i < a.width_p; i += blockDim.x) out[i] = 0;
     return;
   }
   float s = 0.f;
@@ -544,7 +540,7 @@ __global__ __launch_bounds__(256) void batch_norm_mixed(const BatchArgs* __restr
   __syncthreads();
   const float scale = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)a.width + a.epsilon);
   for (int i = threadIdx.x; i < a.width_p; i += blockDim.x)
-    out[i] = i < a.width ? cast<kMixed>(xb[i] * scale * batch_weight<kMixed>(a.weights, w_norm, i)) : 0.f;
+    out[i] = i < a.width ? float_to_half(xb[i] * scale * batch_weight<kMixed>(a.weights, w_norm, i)) : 0;
 }
 
 // Final RMSNorm (cast in mixed mode) and score of every stream (src/cuda/Runtime.cu:380-383;

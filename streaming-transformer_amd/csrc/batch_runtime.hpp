@@ -17,7 +17,7 @@ class Batch {
  private:
   template <int P> void launch_sequence();
   template <int P, int E, bool kNorm, int CT, int SW>
-  void project(const float* X, int ld, uint32_t woff, int N, uint32_t norm, int layer);
+  void project(const void* X, int ld, uint32_t woff, int N, uint32_t norm, int layer);
   int group_tiles(int cols) const;
   bool wide_qkv_ = false, wide_gateup_ = false;  // two column tiles per workgroup
   size_t kv_words_ = 0;                           // one stream's K (or V) ring in 4-byte words
@@ -158,7 +158,7 @@ int Batch::group_tiles(int cols) const {
 }
 
 template <int P, int E, bool kNorm, int CT, int SW>
-void Batch::project(const float* X, int ld, uint32_t woff, int N, uint32_t norm, int layer) {
+void Batch::project(const void* X, int ld, uint32_t woff, int N, uint32_t norm, int layer) {
   const int nt = group_tiles(N / (kBatchTile * CT));
   const dim3 grid(N / (kBatchTile * CT), streams_p_ / kBatchTile / nt), block(64 * kSlices / SW);
   if (nt == 4)
@@ -183,7 +183,7 @@ void Batch::launch_sequence() {
   // Mixed mode casts each norm's output, so its norms run first into xn; the other modes fold
   // the norm into the projection (kNorm).
   constexpr bool kFold = P != kMixed;
-  const float* nx = kFold ? a.x : a.xn;
+  const void* nx = kFold ? a.x : a.xn;
   auto norm = [&](uint32_t w_norm) {
     if constexpr (!kFold)
       hipLaunchKernelGGL(batch_norm_mixed, dim3(streams_p_), dim3(256), 0, stream_, dargs_, w_norm);
