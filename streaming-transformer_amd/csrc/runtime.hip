@@ -238,6 +238,8 @@ class Runtime {
   void check_device_error();
   void sync() { HIP_CHECK(hipStreamSynchronize(stream_)); }
   bool persistent() const { return opt_.backend == ST_BACKEND_PERSISTENT; }
+  bool coresident(int grid);
+  bool plain_launch_ = false;  // FUSED: the grid passed the co-residency probe
   bool vendor() const { return opt_.backend == ST_BACKEND_CUBLAS || opt_.backend == ST_BACKEND_CUBLAS_GRAPH; }
   void reset_device();
   void start_worker();
@@ -460,7 +462,44 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
     HIP_CHECK(hipStreamEndCapture(stream_, &graph_));
     HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
   }
+  if (options.backend == ST_BACKEND_FUSED && grid_ > 1) plain_launch_ = coresident(grid_);
   if (persistent()) start_worker();
+}
+
+// Co-residency probe: one plain launch of `grid` workgroups with the fused kernel's footprint
+// (kThreads threads and LdsAll in LDS, which leaves room for one workgroup per CU). Every
+// workgroup counts itself in and waits, for at most 50 ms, until all have arrived. True when
+// they all did: the grid then runs at once without a cooperative launch, whose dispatch costs
+// about 15 us per step on this stack.
+__global__ __launch_bounds__(kThreads) void coresidency_kernel(unsigned* arrived, unsigned grid, unsigned long long ticks,
+                                                                unsigned* failed) {
+  __shared__ LdsAll lds;
+  if (threadIdx.x == 0) {
+    *reinterpret_cast<volatile int*>(&lds.cmd) = (int)blockIdx.x;  // keeps the LDS allocation
+    __hip_atomic_fetch_add(arrived, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long start = wall_clock64();
+    while (__hip_atomic_load(arrived, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < grid) {
+      if (wall_clock64() - start > ticks) {
+        __hip_atomic_fetch_or(failed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(8);
+    }
+  }
+}
+
+bool Runtime::coresident(int grid) {
+  DeviceBuffer words;
+  words.alloc(256);
+  HIP_CHECK(hipMemset(words.ptr, 0, 256));
+  unsigned* w = reinterpret_cast<unsigned*>(words.ptr);
+  const unsigned long long ticks = (unsigned long long)wall_khz_ * 50ull;  // 50 ms
+  hipLaunchKernelGGL(coresidency_kernel, dim3(grid), dim3(kThreads), 0, stream_, w, (unsigned)grid, ticks, w + 32);
+  HIP_CHECK(hipGetLastError());
+  sync();
+  unsigned failed = 0;
+  HIP_CHECK(hipMemcpy(&failed, w + 32, 4, hipMemcpyDeviceToHost));
+  return failed == 0;
 }
 
 Runtime::~Runtime() {
@@ -612,8 +651,9 @@ void Runtime::launch_phases() {
 
 template <int P, int A>
 void Runtime::launch_fused_t(const float* event) {
-  if (grid_ == 1) {
-    hipLaunchKernelGGL((fused_kernel<P, A>), dim3(1), dim3(kThreads), 0, stream_, dargs_, event);
+  if (grid_ == 1 || plain_launch_) {
+    // One workgroup, or a grid the co-residency probe showed to be resident all at once.
+    hipLaunchKernelGGL((fused_kernel<P, A>), dim3(grid_), dim3(kThreads), 0, stream_, dargs_, event);
   } else {
     void* params[] = {&dargs_, &event};
     HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<void*>(fused_kernel<P, A>), dim3(grid_),
@@ -1183,7 +1223,9 @@ std::string Runtime::info() {
   o << "{\"environment\": " << probe_ << ", \"backend\": \"" << backends[opt_.backend]
     << "\", \"precision\": \"" << precs[prec_] << "\", \"blocks\": " << grid_
     << ", \"threads\": " << kThreads << ", \"legal_cooperative_blocks\": " << legal_blocks_
-    << ", \"resource_kernel\": \"" << name << "\", \"registers_per_thread\": " << fa.numRegs
+    << ", \"fused_launch\": \""
+    << (opt_.backend != ST_BACKEND_FUSED ? "n/a" : plain_launch_ || grid_ == 1 ? "plain" : "cooperative")
+    << "\", \"resource_kernel\": \"" << name << "\", \"registers_per_thread\": " << fa.numRegs
     << ", \"local_bytes\": " << fa.localSizeBytes << ", \"shared_bytes\": " << fa.sharedSizeBytes
     << ", \"phases_per_step\": " << 5 * c_.layers + 2 << ", \"prefetch_slabs\": " << kPF
     << ", \"attention_chunk\": " << args_.chunk << ", \"weight_arena_bytes\": " << args_.weight_bytes
