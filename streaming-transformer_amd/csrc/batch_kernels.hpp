@@ -363,6 +363,10 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
       const unsigned long long pos = a.position[b];
       float va = s0, vb = s1;
       if (sec < 2) {
+        // No FMA contraction here: left to the compiler, it fuses one product or the other
+        // depending on the kernel variant, and a stream's bits would then depend on the
+        // workgroup shape chosen for its batch size.
+#pragma clang fp contract(off)
         const int e = i % a.dim;
         const float angle = (float)pos * a.rope_freq[e >> 1];
         const float co = cosf(angle), si = sinf(angle);

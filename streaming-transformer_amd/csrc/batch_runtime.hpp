@@ -172,14 +172,16 @@ void Batch::project(const void* X, int ld, uint32_t woff, int N, uint32_t norm, 
                        norm, layer);
 }
 
-// The wide projections (QKV, gate/up) take two column tiles and two K-slices per wave, which
-// halves the X reads at large batches and still leaves many workgroups at small ones; the
-// narrow ones (input, OUT, down: d outputs) keep one of each for parallelism. The choice
-// depends on the shape only, never on B.
+// Workgroup shapes per projection. Every shape computes the same fixed slice tree, so the
+// choice changes speed only, never a stream's bits. Small batches want many workgroups (one
+// column tile and one K-slice per wave); large ones want each X fragment reused across column
+// tiles: from 64 streams the wide projections (QKV, gate/up) take two column tiles and two
+// K-slices per wave, and from 128 streams the narrow ones (OUT, down) take two column tiles.
 template <int P>
 void Batch::launch_sequence() {
   const BatchArgs& a = args_;
   const int d = c_.width, F = c_.ffn;
+  const bool wide = streams_p_ >= 64, narrow = streams_p_ >= 128 && (c_.width / kBatchTile) % 2 == 0;
   // Mixed mode casts each norm's output, so its norms run first into xn; the other modes fold
   // the norm into the projection (kNorm).
   constexpr bool kFold = P != kMixed;
@@ -192,15 +194,17 @@ void Batch::launch_sequence() {
   for (int l = 0; l < c_.layers; l++) {
     const LayerWeights& w = a.layer[l];
     norm(w.norm1);
-    if (wide_qkv_) project<P, kEpQkv, kFold, 2, 2>(nx, a.width_p, w.qkv, 3 * d, w.norm1, l);
+    if (wide && wide_qkv_) project<P, kEpQkv, kFold, 2, 2>(nx, a.width_p, w.qkv, 3 * d, w.norm1, l);
     else project<P, kEpQkv, kFold, 1, 1>(nx, a.width_p, w.qkv, 3 * d, w.norm1, l);
     hipLaunchKernelGGL(batch_attention<P>, dim3(streams_ * c_.heads), dim3(kAttnThreads), (size_t)c_.window * 4,
                        stream_, dargs_, l);
-    project<P, kEpOut, false, 1, 1>(a.attn, a.width_p, w.out, d, 0u, l);
+    if (narrow) project<P, kEpOut, false, 2, 1>(a.attn, a.width_p, w.out, d, 0u, l);
+    else project<P, kEpOut, false, 1, 1>(a.attn, a.width_p, w.out, d, 0u, l);
     norm(w.norm2);
-    if (wide_gateup_) project<P, kEpGateUp, kFold, 2, 2>(nx, a.width_p, w.gateup, 2 * F, w.norm2, l);
+    if (wide && wide_gateup_) project<P, kEpGateUp, kFold, 2, 2>(nx, a.width_p, w.gateup, 2 * F, w.norm2, l);
     else project<P, kEpGateUp, kFold, 1, 1>(nx, a.width_p, w.gateup, 2 * F, w.norm2, l);
-    project<P, kEpDown, false, 1, 1>(a.act, a.ffn_p, w.down, d, 0u, l);
+    if (narrow) project<P, kEpDown, false, 2, 1>(a.act, a.ffn_p, w.down, d, 0u, l);
+    else project<P, kEpDown, false, 1, 1>(a.act, a.ffn_p, w.down, d, 0u, l);
   }
   hipLaunchKernelGGL(batch_final<P>, dim3(streams_), dim3(64), 0, stream_, dargs_);
   HIP_CHECK(hipGetLastError());

@@ -88,17 +88,19 @@ def test_bf16_weights_match_oracle_on_rounded_weights():
             _check_state(rt.snapshot(b), oracles[b].snapshot())
 
 
-@pytest.mark.parametrize('weight_dtype,mixed', [(WeightStorage.AS_MODEL, False), (WeightStorage.BF16, False),
-                                                (WeightStorage.AS_MODEL, True)])
-def test_stream_independent_of_batch(weight_dtype, mixed):
+@pytest.mark.parametrize('weight_dtype,mixed,streams,steps', [
+    (WeightStorage.AS_MODEL, False, 40, 70), (WeightStorage.BF16, False, 40, 70), (WeightStorage.AS_MODEL, True, 40, 70),
+    # 130 streams: the large-batch workgroup shapes of every projection
+    (WeightStorage.BF16, False, 130, 20), (WeightStorage.AS_MODEL, True, 130, 20)])
+def test_stream_independent_of_batch(weight_dtype, mixed, streams, steps):
     c = SHAPES['small']
     w = synthetic_checkpoint(c, seed=13, mixed=mixed)
-    steps, streams = 70, 40
     events = _events(c, 13, steps, streams)
+    picks = (0, 21, streams - 1)
     with batch((c, w, mixed), streams, weight_dtype) as rt:
         many = np.stack([rt.step(events[i]) for i in range(steps)])
-        states = [rt.snapshot(b) for b in (0, 21, 39)]
-    for b, state in zip((0, 21, 39), states):
+        states = [rt.snapshot(b) for b in picks]
+    for b, state in zip(picks, states):
         with batch((c, w, mixed), 1, weight_dtype) as one:
             alone = np.array([one.step(events[i, b:b + 1])[0] for i in range(steps)], dtype=np.float32)
             np.testing.assert_array_equal(alone, many[:, b])
