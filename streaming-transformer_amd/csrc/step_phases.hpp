@@ -1476,8 +1476,22 @@ __global__ __launch_bounds__(kThreads) void persistent_kernel(const StepArgs* __
         }
         cmd = __shfl(cmd, 0);
         seq = ((unsigned long long)(unsigned)__shfl((int)(got >> 32), 0) << 32) | (unsigned)__shfl((int)got, 0);
-        if (cmd == kCmdRun)
-          for (int i = c.lane; i < a.features_p; i += 64) c.tstore(a.t_in + (uint32_t)i, base, i < a.features ? a.mapped_input[i] : 0.f);
+        if (cmd == kCmdRun) {
+          // The event crosses PCIe: issue all of a lane's loads (features_p <= 1024, so at
+          // most 16) before any store, one round trip instead of one per element.
+          constexpr int kIn = 1024 / 64;
+          float v[kIn];
+#pragma unroll
+          for (int j = 0; j < kIn; j++) {
+            const int i = c.lane + 64 * j;
+            v[j] = i < a.features ? a.mapped_input[i] : 0.f;
+          }
+#pragma unroll
+          for (int j = 0; j < kIn; j++) {
+            const int i = c.lane + 64 * j;
+            if (i < a.features_p) c.tstore(a.t_in + (uint32_t)i, base, v[j]);
+          }
+        }
         if (c.lane == 0) c.tstore(a.t_cmd, base, __builtin_bit_cast(float, cmd));
       }
       // Every workgroup waits for the command (as long as the coordinator may wait, and then
