@@ -1,7 +1,8 @@
 """Python wrapper of the C oracle (oracle/stream_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg, always as the checker. The product path never imports this module.
+cpu_baseline leg, always as the reference the GPU results are compared with. The product
+path never imports this module.
 """
 from __future__ import annotations
 

@@ -1,7 +1,7 @@
 /*
  * CPU oracle: plain-C restatement of the reference CPU step.
  *
- * TEST INFRASTRUCTURE ONLY (the checker, never the product): loaded by tests/,
+ * TEST INFRASTRUCTURE ONLY (a reference for comparison, never the product): loaded by tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg.
  *
  * Follows, function by function:
@@ -16,7 +16,7 @@
  * Pinning (each check lives in tests/):
  *   - end-to-end against the reference's golden vectors fixtures/small-{fp32,mixed}/expected
  *     (201 events, eviction, several ring revolutions, warm reset): test_oracle_golden.py;
- *   - the float and double accumulation variants against each other at BASELINE shapes;
+ *   - the float and double accumulation variants against each other at the Small, Main and Large shapes;
  *   - an independent numpy FullSequence local-causal masked forward (reference/model.py:140-160),
  *     which shares no ring/position logic with this file: test_oracle_invariants.py;
  *   - closed forms: adjacent-pair RoPE (tests/test_porting_contract.py:10-21), zero Q/K =>

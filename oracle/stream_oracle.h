@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the streaming local-causal transformer step.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker: only tests/,
+ * TEST INFRASTRUCTURE ONLY. This library is the reference for comparison: only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it. The
  * product path (libstamd.so) never links or calls it.
  *

@@ -7,7 +7,7 @@ bench/Main.cpp:57-84 as used at :354-409:
   mixed: |a - r| <= 0.002 (l+1) max(1, RMS(vector)) + 0.02 |r| per hidden / KV vector,
          complete per-layer state relative L2 <= 0.002; scores |a - r| <= 0.002 L + 0.02 |r|
          and RMS(score error) / max(1, RMS(scores)) <= 0.002 (docs/NumericalPolicy.md:5-20).
-The tighter FP32 gate used by this build's tests, |a - r| <= 1e-6 + 1e-5 |r|, is
+The tighter FP32 gate used by the GPU parity tests, |a - r| <= 1e-6 + 1e-5 |r|, is
 :func:`fp32_strict_failures`.
 """
 from __future__ import annotations

@@ -1,4 +1,4 @@
-"""Pin the oracle where the golden fixtures leave it open (dh = 64, BASELINE shapes, long
+"""Pin the oracle where the golden fixtures leave it open (dh = 64, the Small/Main/Large shapes, long
 positions, FP16/BF16 rounding), using checks the mathematics fixes rather than a retyped
 formula:
 
@@ -11,7 +11,7 @@ formula:
   (tests/test_porting_contract.py:24-51);
 - zero input => score exactly 0 (tests/Lifecycle.cu:38,60-62);
 - roundHalf KAT (tests/Native.cpp:20-21) and the FP16/BF16 rounders against numpy/torch;
-- float vs double accumulation at BASELINE shapes.
+- float vs double accumulation at the Small/Main/Large shapes.
 """
 import numpy as np
 import pytest

@@ -72,7 +72,7 @@ def _stream(config, seed, count):
 
 
 SHAPES = {
-    # BASELINE configurations with features = d_model (SwiGLU, RoPE, norm weights 1)
+    # the Small, Main and Large configurations with features = d_model (SwiGLU, RoPE, norm weights 1)
     'small': ModelConfig(4, 256, 4, 1024, 64, 256),
     'main': ModelConfig(8, 512, 8, 2048, 128, 512),
     'large': ModelConfig(12, 1024, 16, 4096, 512, 1024),
