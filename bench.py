@@ -366,6 +366,15 @@ def main():
             extra['persistent_service_p50_us'] = nearest_rank(host, 0.5)
             extra['persistent_service_p99_us'] = nearest_rank(host, 0.99)
 
+    if not args.quick and backend == Backend.FUSED:
+        # The reference's default backend (a captured step per event): here the hipGraph holds
+        # the fused kernel as one node.
+        gopts = RuntimeOptions(backend=Backend.GRAPH, blocks=0, weight_dtype=opts.weight_dtype)
+        with Runtime((c, weights, mixed), gopts) as rt:
+            rt.device_run(events[:fill], reset=True)
+            _, gper = rt.device_run(events[fill:fill + min(args.steps, 512)])
+        extra['graph_p50_us'] = nearest_rank(gper, 0.5)
+        extra['graph_p99_us'] = nearest_rank(gper, 0.99)
     if not args.quick and args.precision != 'bf16w':
         # The same workload through the vendor GEMV baseline (rocBLAS projections, captured).
         vopts = RuntimeOptions(backend=Backend.CUBLAS_GRAPH, blocks=0)
@@ -418,6 +427,8 @@ def main():
                 'roofline_us_per_step': bytes_step / (HBM_PEAK_GBS * 1e9) * 1e6,
                 'kernel': {Backend.FUSED: 'fused_kernel', Backend.CUBLAS: 'rocBLAS gemv + stage kernels',
                            Backend.CUBLAS_GRAPH: 'rocBLAS gemv + stage kernels'}.get(backend, 'phase_kernel sequence')}
+    if backend == Backend.GRAPH and info.get('fused_launch', '').startswith('graph node'):
+        roofline['kernel'] = 'fused_kernel (graph node)'
     roofline['traffic'] = traffic_per_launch(
         ROOT / 'profiles' / f'traffic_{args.backend}_kernel_{args.config}_{args.precision}.md')
     roofline['frac_p50'] = round(bytes_step / (p50 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)

@@ -30,8 +30,10 @@ enum {
   ST_ERR_NUMERIC = 4    /* device-side watchdog (barrier timeout) tripped */
 };
 
-/* Stream::Backend (include/Runtime.hpp:7). CUDA = staged HIP kernels, GRAPH = the staged
- * sequence captured in a hipGraph, FUSED = one cooperative launch per step, PERSISTENT =
+/* Stream::Backend (include/Runtime.hpp:7). CUDA = staged HIP kernels, GRAPH = one step
+ * captured in a hipGraph (the fused kernel as a single node when blocks > 1 and the grid
+ * passes the co-residency probe, otherwise the staged sequence; st_runtime_info's
+ * "fused_launch" says which), FUSED = one launch of the fused kernel per step, PERSISTENT =
  * resident kernel driven through a host mailbox. CUBLAS / CUBLAS_GRAPH are the vendor GEMV
  * baselines (src/cuda/Runtime.cu:330-385): the projections run in rocBLAS (sgemv for FP32,
  * gemm_ex FP16 -> FP32 for mixed), eagerly or captured in a hipGraph; they take the
@@ -131,7 +133,7 @@ int st_runtime_device_trace(st_runtime* runtime, const float* inputs, size_t cou
 
 /* Extension (no counterpart in the reference): per-launch device timing. Runs `count`
  * events from a preloaded device copy, one step per launch (FUSED: one cooperative launch
- * per event; CUDA/GRAPH: device-to-device staging copy plus the phase sequence), after a
+ * per event; CUDA/GRAPH: device-to-device staging copy plus the staged step), after a
  * reset if `reset` is nonzero, otherwise continuing the current stream state. A HIP event
  * is recorded on the runtime's stream after every step; per_event_us (may be NULL)
  * receives the count event-to-event durations, *us_per_event their mean. */

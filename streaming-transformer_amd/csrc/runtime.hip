@@ -239,7 +239,8 @@ class Runtime {
   void sync() { HIP_CHECK(hipStreamSynchronize(stream_)); }
   bool persistent() const { return opt_.backend == ST_BACKEND_PERSISTENT; }
   bool coresident(int grid);
-  bool plain_launch_ = false;  // FUSED: the grid passed the co-residency probe
+  bool plain_launch_ = false;  // FUSED (and GRAPH's fused node): the grid passed the co-residency probe
+  bool graph_fused_ = false;   // GRAPH: the captured step is the fused kernel
   bool vendor() const { return opt_.backend == ST_BACKEND_CUBLAS || opt_.backend == ST_BACKEND_CUBLAS_GRAPH; }
   void reset_device();
   void start_worker();
@@ -453,12 +454,20 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
     }
   }
   if (options.backend == ST_BACKEND_GRAPH) {
-    // Warm up outside capture, restore the initial state, then capture the phase sequence.
-    launch_phases();
+    // The graph holds one step: the fused kernel as a single plain node when the grid is
+    // resident all at once (bit-identical to the phase sequence), else the phase sequence.
+    // Warm up outside capture, restore the initial state, then capture.
+    graph_fused_ = grid_ > 1 && grid_ <= legal_blocks_ && coresident(grid_);
+    if (graph_fused_) plain_launch_ = true;
+    auto sequence = [&] {
+      if (graph_fused_) launch_fused();
+      else launch_phases();
+    };
+    sequence();
     sync();
     reset_device();
     HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
-    launch_phases();
+    sequence();
     HIP_CHECK(hipStreamEndCapture(stream_, &graph_));
     HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
   }
@@ -1224,7 +1233,8 @@ std::string Runtime::info() {
     << "\", \"precision\": \"" << precs[prec_] << "\", \"blocks\": " << grid_
     << ", \"threads\": " << kThreads << ", \"legal_cooperative_blocks\": " << legal_blocks_
     << ", \"fused_launch\": \""
-    << (opt_.backend != ST_BACKEND_FUSED ? "n/a" : plain_launch_ || grid_ == 1 ? "plain" : "cooperative")
+    << (opt_.backend == ST_BACKEND_GRAPH ? (graph_fused_ ? "graph node (plain)" : "n/a (phase sequence)")
+        : opt_.backend != ST_BACKEND_FUSED ? "n/a" : plain_launch_ || grid_ == 1 ? "plain" : "cooperative")
     << "\", \"resource_kernel\": \"" << name << "\", \"registers_per_thread\": " << fa.numRegs
     << ", \"local_bytes\": " << fa.localSizeBytes << ", \"shared_bytes\": " << fa.sharedSizeBytes
     << ", \"phases_per_step\": " << 5 * c_.layers + 2 << ", \"prefetch_slabs\": " << kPF

@@ -16,7 +16,10 @@ from streamtx import (Backend, ModelConfig, Runtime, RuntimeOptions, WeightStora
 pytestmark = pytest.mark.gpu
 
 STRICT = dict(atol=1e-6, rtol=1e-5)
-BACKENDS = [(Backend.CUDA, 0), (Backend.GRAPH, 0), (Backend.FUSED, 1), (Backend.FUSED, 4), (Backend.FUSED, 0)]
+# GRAPH with a full grid captures the fused kernel as one node; with one workgroup it captures
+# the staged phase sequence.
+BACKENDS = [(Backend.CUDA, 0), (Backend.GRAPH, 0), (Backend.GRAPH, 1), (Backend.FUSED, 1), (Backend.FUSED, 4),
+            (Backend.FUSED, 0)]
 # Vendor GEMV baselines (rocBLAS projections): same parity bars, their own summation order.
 VENDOR = [(Backend.CUBLAS, 0), (Backend.CUBLAS_GRAPH, 0)]
 
@@ -197,8 +200,14 @@ def test_cooperative_grid_limit_and_info():
     assert info['environment']['arch'].startswith('gfx950')
     assert info['blocks'] == info['environment']['compute_units']
     assert info['legal_cooperative_blocks'] >= info['blocks']
+    assert info['fused_launch'] in ('plain', 'cooperative')
     with pytest.raises(RuntimeError, match='occupancy limit'):
         Runtime((c, w, False), RuntimeOptions(backend=Backend.FUSED, blocks=info['legal_cooperative_blocks'] + 1))
+    with runtime((c, w, False), Backend.GRAPH, 0) as rt:
+        assert rt.info()['fused_launch'] == ('graph node (plain)' if info['fused_launch'] == 'plain'
+                                             else 'n/a (phase sequence)')
+    with runtime((c, w, False), Backend.GRAPH, 1) as rt:
+        assert rt.info()['fused_launch'] == 'n/a (phase sequence)'
 
 
 def test_stopped_runtime_rejects_commands():
