@@ -521,6 +521,18 @@ __device__ __forceinline__ void prefetch_matvec(Ctx<P>& c, const WaveWork& w, Sl
 struct AttnWork {
   int wid, nw, items, nch;  // items owned by this wave; chunks per head
   int kchunks;              // 16-byte chunks of one K (or V) block
+  int heads;
+  // Items are numbered chunk-major: item it covers chunk it / heads of head it % heads. The
+  // chunks of one head then fall on workgroups whose indices agree modulo `heads` (with a
+  // grid and a head count that are multiples of 8, on one XCD under round-robin dispatch),
+  // and the waves that combine heads (chunk 0) sit in different workgroups.
+  __device__ __forceinline__ void decode(int it, int& h, int& ch) const {
+    ch = it / heads;
+    h = it - ch * heads;
+  }
+  // Index of the (head, chunk) partial in t_po / t_pm / t_ps: head-major, so that a head's
+  // partials are contiguous for its combine.
+  __device__ __forceinline__ uint32_t partial(int h, int ch) const { return (uint32_t)(h * nch + ch); }
 };
 
 template <int P>
@@ -532,6 +544,7 @@ __device__ __forceinline__ AttnWork attn_work(const StepArgs& a, int grid, int g
   int total = a.heads * w.nch;
   w.items = total > w.wid ? (total - w.wid + w.nw - 1) / w.nw : 0;
   w.kchunks = (a.chunk * a.dim * Traits<P>::kKvBytes + 15) / 16;
+  w.heads = a.heads;
   return w;
 }
 
@@ -556,7 +569,8 @@ __device__ __forceinline__ void prefetch(Ctx<P>& c, Phase p, uint4 (&ring)[kPF])
   if (p.kind == kAttn) {
     AttnWork w = attn_work<P>(c.a, c.grid, c.g, sw);
     if (w.items == 0) return;
-    int h = w.wid / w.nch, ch = w.wid - h * w.nch;
+    int h, ch;
+    w.decode(w.wid, h, ch);
     load_block<P>(c, c.kr, p.layer, h, ch, w.kchunks, ring);
     load_block<P>(c, c.vr, p.layer, h, ch, w.kchunks, ring + kKB);
   } else if (p.kind != kFinal) {
@@ -624,11 +638,16 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* 
   if (w.slabs == 0) return;
   int ru = 0, s = 0;  // row within the unit, slab within the row
   float acc0 = 0.f, acc1 = 0.f;
-  float su0 = 0.f, su1 = 0.f;  // lane k: row sums of the k-th unit finished in this ring pass
+  // Lane k holds the row sums of the k-th unit finished since the last epilogue batch. The
+  // epilogues (whose tagged stores are written through to memory) run after the ring loop:
+  // the loop's back edge and exit wait for every outstanding vector memory operation of
+  // the wave (vmcnt(0)), and stores issued inside the loop would make the wave wait for
+  // their write acknowledgements before it signals completion and prefetches the next phase.
+  float su0 = 0.f, su1 = 0.f;
+  int finished = 0;
   const float* xs = xs_buf + c.lane * Traits<P>::kEpc;
   if (c.wave == 1) stamp(c, p, 4);
   for (int base = 0; base < w.slabs; base += kPF) {
-    int finished = 0;  // units completed in this pass of the ring
 #pragma unroll
     for (int j = 0; j < kPF; j++) {
       if (base + j < w.slabs) {
@@ -659,17 +678,23 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* 
         }
       }
     }
-    // Epilogues of the finished units, one unit per lane, outside the unrolled loop.
-    if (c.lane < finished) epilogue(c, p, unit + kStreamWaves * c.lane, su0, su1, xres);
-    unit += kStreamWaves * finished;
+    // At most kPF units finish in one pass (a unit has at least one slab): flush the batch
+    // inside the loop only when the next pass could overflow the 64 lanes (very small grids).
+    if (finished > 64 - kPF) {
+      if (c.lane < finished) epilogue(c, p, unit + kStreamWaves * c.lane, su0, su1, xres);
+      unit += kStreamWaves * finished;
+      finished = 0;
+    }
   }
+  // Epilogues of the finished units, one unit per lane.
+  if (c.lane < finished) epilogue(c, p, unit + kStreamWaves * c.lane, su0, su1, xres);
   if (c.wave == 1) stamp(c, p, 6);
 }
 
 // ---------------------------------------------------------------------------------------------
 // stream waves: attention (src/cuda/Primitives.cuh:167-219, src/cpu/Cpu.cpp:97-109)
 
-// Publish the (max logit, exp sum) of item `it` as tagged elements t_pm / t_ps[it]; the
+// Publish the (max logit, exp sum) of partial `it` as tagged elements t_pm / t_ps[it]; the
 // item's o[dim] goes to t_po[it * dim ..].
 template <int P>
 __device__ __forceinline__ void publish_stats(Ctx<P>& c, unsigned ep, int it, float m, float s) {
@@ -814,8 +839,8 @@ __device__ __forceinline__ void combine_head(Ctx<P>& c, int layer, int h, int nc
 template <int P>
 __device__ __forceinline__ void combine_owned(Ctx<P>& c, Phase p, const AttnWork& w, int nactive) {
   for (int m = 0; m < w.items; m++) {
-    int it = w.wid + w.nw * m;
-    int h = it / w.nch, ch = it - h * w.nch;
+    int h, ch;
+    w.decode(w.wid + w.nw * m, h, ch);
     if (ch == 0) combine_head(c, p.layer, h, w.nch, nactive);
   }
 }
@@ -874,9 +899,10 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
   const float div = sqrtf((float)dim);
   const unsigned ep_qkv = c.epoch(ph_index(kQkv, p.layer));
   for (int m = 0; m < w.items; m++) {
-    int it = w.wid + w.nw * m;
-    int h = it / w.nch, ch = it - h * w.nch;
+    int h, ch;
+    w.decode(w.wid + w.nw * m, h, ch);
     if (ch >= nactive) continue;
+    const uint32_t pi = w.partial(h, ch);
     // The K and V blocks: the first item's from the LDS stage (loaded by the control wave
     // during the QKV phase) or from the ring (prefetched); later items' from memory.
     uint4 kb[kKB], vb[kKB];
@@ -978,11 +1004,11 @@ __device__ __forceinline__ void compute_attn_regs(Ctx<P>& c, Phase p, uint4 (&ri
       out[e] = column_sum(out[e], group);
     const unsigned ep = c.epoch(ph_index(kAttn, p.layer));
     if (c.lane < group) {
-      const uint32_t ob = (uint32_t)it * (uint32_t)dim + (uint32_t)col0;
+      const uint32_t ob = pi * (uint32_t)dim + (uint32_t)col0;
 #pragma unroll
       for (int e = 0; e < E; e++) c.tstore(a.t_po + ob + (uint32_t)e, ep, out[e]);
     }
-    publish_stats(c, ep, it, mx, total);
+    publish_stats(c, ep, pi, mx, total);
     if (c.wave == 1) stamp(c, p, 5);
   }
   combine_owned(c, p, w, nactive);
@@ -1038,9 +1064,10 @@ __device__ __forceinline__ void compute_attn_lds(Ctx<P>& c, Phase p, uint4 (&rin
   const int nactive = (c.valid + chunk - 1) / chunk;
   const float div = sqrtf((float)dim);
   for (int m = 0; m < w.items; m++) {
-    int it = w.wid + w.nw * m;
-    int h = it / w.nch, ch = it - h * w.nch;
+    int h, ch;
+    w.decode(w.wid + w.nw * m, h, ch);
     if (ch >= nactive) continue;
+    const uint32_t pi = w.partial(h, ch);
     if (m > 0) {
       load_block<P>(c, c.kr, p.layer, h, ch, w.kchunks, ring);
       load_block<P>(c, c.vr, p.layer, h, ch, w.kchunks, ring + kKB);
@@ -1075,9 +1102,9 @@ __device__ __forceinline__ void compute_attn_lds(Ctx<P>& c, Phase p, uint4 (&rin
     for (int i = c.lane; i < dim; i += 64) {
       float o = 0.f;
       for (int j = 0; j < rows; j++) o += probs[j] * stage[j * stride + i];
-      c.tstore(a.t_po + (uint32_t)it * (uint32_t)dim + (uint32_t)i, ep, o);
+      c.tstore(a.t_po + pi * (uint32_t)dim + (uint32_t)i, ep, o);
     }
-    publish_stats(c, ep, it, mx, total);
+    publish_stats(c, ep, pi, mx, total);
     __builtin_amdgcn_wave_barrier();
   }
   combine_owned(c, p, w, nactive);
@@ -1182,7 +1209,8 @@ __device__ __forceinline__ void load_kv_to_lds(Ctx<P>& c, int layer) {
   for (int sw = 0; sw < kStreamWaves; sw++) {
     const AttnWork w = attn_work<P>(a, c.grid, c.g, sw);
     if (w.items == 0) break;  // items go to waves in order: none for later waves either
-    const int h = w.wid / w.nch, ch = w.wid - h * w.nch;
+    int h, ch;
+    w.decode(w.wid, h, ch);
     if (ch >= nactive) continue;
     float* st = c.lds.stage[sw];
 #pragma unroll
