@@ -36,18 +36,6 @@ constexpr int kStreamWaves = kWaves - 1;
 #ifndef STAMD_PF
 #define STAMD_PF 8
 #endif
-#ifndef STAMD_OUT_EARLY
-#define STAMD_OUT_EARLY 0
-#endif
-#ifndef STAMD_PACE
-#define STAMD_PACE 0
-#endif
-#ifndef STAMD_NOPF
-#define STAMD_NOPF 0
-#endif
-#ifndef STAMD_SYNC_PF
-#define STAMD_SYNC_PF 0
-#endif
 constexpr int kPF = STAMD_PF;      // register ring depth (slabs) per stream wave
 constexpr int kKB = kPF >= 16 ? 8 : kPF / 2;  // ring slabs per attention K (or V) block
 static_assert(2 * kKB <= kPF, "an attention item's K and V blocks fit in the ring");

@@ -39,7 +39,6 @@ struct LdsAll {
   float rope_sin[kMaxDim / 2];
   WaveSplit split[kStreamWaves][kFinal];  // per stream wave and matvec kind (forward only)
   unsigned done[2];                      // stream waves finished with the phase of this parity
-  unsigned issued;                       // stream-wave phases whose results are issued, this forward
   unsigned helped;                       // epoch of the wide vector whose odd chunks the helper staged
   int cmd;                               // persistent worker: the current mailbox command
   unsigned stamps[kStampPhases][kStamps];  // profiling: low 32 bits of the wall clock
@@ -511,9 +510,6 @@ __device__ __forceinline__ void prefetch_matvec(Ctx<P>& c, const WaveWork& w, Sl
   for (int j = 0; j < kPF; j++) {
     ring[j] = ld16(c.wr, (j < w.slabs ? cur : last).offset(c.lane));
     cur.advance(w);
-#if STAMD_PACE
-    __builtin_amdgcn_s_sleep(STAMD_PACE);
-#endif
   }
 }
 
@@ -1281,40 +1277,23 @@ __device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
   const bool stamps = a.stamps && c.wave == 1 && c.lane == 0;
   fill_split(c);
   uint4 ring[kPF];
-#if !STAMD_NOPF
   prefetch(c, phase_of(a, 0), ring);
-#endif
   for (int ph = 0; ph < nph; ph++) {
     lds_barrier();
     Phase p = phase_of(a, ph);
     if (p.kind == kFinal) break;
-#if STAMD_NOPF
-    prefetch(c, p, ring);
-#endif
     compute<P, A>(c, p, ph & 1, ring);
     if (stamps) lstamp(c, ph, 1);
     // Signal before issuing the next phase's prefetch: the issue itself can stall on a
     // full memory pipeline, and the control wave can stage meanwhile.
     if (c.lane == 0) __hip_atomic_fetch_add(&c.lds.done[ph & 1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-#if STAMD_SYNC_PF
-    if (c.lane == 0) __hip_atomic_fetch_add(&c.lds.issued, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    while (__hip_atomic_load(&c.lds.issued, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)(kStreamWaves * (ph + 1)))
-      __builtin_amdgcn_s_sleep(1);
-#endif
-#if !STAMD_NOPF
     {
       // With the attention K/V in LDS the ring has nothing to prefetch for attention. It
       // stays empty, so that the attention phase's stores and polls find this CU's memory
       // queue empty; OUT is prefetched after attention.
       const Phase nxt = phase_of(a, ph + 1);
-#if STAMD_OUT_EARLY
-      if (A == 1 && c.kv_lds && nxt.kind == kAttn) prefetch(c, phase_of(a, ph + 2), ring);
-      else if (!(A == 1 && c.kv_lds && p.kind == kAttn)) prefetch(c, nxt, ring);
-#else
       if (!(A == 1 && c.kv_lds && nxt.kind == kAttn)) prefetch(c, nxt, ring);
-#endif
     }
-#endif
     if (c.wave == kWaves - 1) help_stage(c, phase_of(a, ph + 1), (ph + 1) & 1);
     if (stamps) lstamp(c, ph, 7);
   }
@@ -1328,7 +1307,6 @@ __device__ __forceinline__ void forward(Ctx<P>& c) {
   if (threadIdx.x == 0) {
     c.lds.done[0] = 0;
     c.lds.done[1] = 0;
-    c.lds.issued = 0;
     c.lds.helped = ~0u;
   }
   fill_rope(c);
