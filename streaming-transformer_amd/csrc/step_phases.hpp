@@ -740,10 +740,13 @@ __device__ __forceinline__ void combine_head(Ctx<P>& c, int layer, int h, int nc
     const float big = wave_top(c.lane < nactive ? mc : -INFINITY);
     const float e = c.lane < nactive ? expf(mc - big) : 0.f;
     const float denom = wave_total(sc * e);
+    // No per-chunk branch: chunks at or beyond nactive have e = 0 (lanes >= nactive) and
+    // hold the clamped, current partial of chunk nactive - 1, so their terms are exact zeros
+    // and the chunk-order sum is unchanged. (A branch per chunk made the compiler precompute
+    // and spill 32 predicates and serialize the loop on them: about 1.4 us per combine.)
     float o = 0.f;
 #pragma unroll
-    for (int k = 0; k < kCombineOne; k++)
-      if (k < nactive) o += __builtin_bit_cast(float, po[k].x) * lane_value(e, k);
+    for (int k = 0; k < kCombineOne; k++) o += __builtin_bit_cast(float, po[k].x) * lane_value(e, k);
     if (c.lane < dim) c.tstore(a.t_attn + h * dim + c.lane, ep, cast<P>(o / denom));
     return;
   }
@@ -779,9 +782,9 @@ __device__ __forceinline__ void combine_head(Ctx<P>& c, int layer, int h, int nc
         if (__all(ok) || c.dead || c.expired(start)) break;
         __builtin_amdgcn_s_sleep(kPollSleep);
       }
+      // Chunks at or beyond nactive add exact zeros (e = 0 there), as in the one-pass path.
 #pragma unroll
-      for (int k = 0; k < 8; k++)
-        if (k0 + k < nactive) o += __builtin_bit_cast(float, po[k].x) * lane_value(e, k0 + k);
+      for (int k = 0; k < 8; k++) o += __builtin_bit_cast(float, po[k].x) * lane_value(e, k0 + k);
     }
     if (c.lane < dim) c.tstore(a.t_attn + h * dim + c.lane, ep, cast<P>(o / denom));
     return;
