@@ -163,13 +163,22 @@ __device__ __forceinline__ void poll_regs(Ctx<P>& c, uint32_t tv, int n, int p0,
 #pragma unroll
     for (int k = 0; k < NP; k++)
       buf[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(c.tr, (int)voff, 1024 * k, kSc1));
+    // The epoch check. Staging polls (up to 8 pieces per lane) use bitwise operators, which
+    // compile to lane-mask arithmetic; a short-circuit check compiled to one divergent branch
+    // per piece and kept every pass long. Wide polls (16 pieces per lane: the FFN vector) keep
+    // the short-circuit form. Measured Large p50: bitwise everywhere 381 us, short-circuit
+    // everywhere 380 us, this split 362 us; why the wide polls prefer it is not pinned down.
     bool ok = true;
 #pragma unroll
     for (int k = 0; k < NP; k++) {
-      int pc = c.lane + 64 * k;
-      int e0 = 2 * (p0 + pc);
-      bool in = pc < np;
-      ok = ok && (!in || ((e0 >= n || buf[k].y == ep) && (e0 + 1 >= n || buf[k].w == ep)));
+      const int pc = c.lane + 64 * k;
+      const int e0 = 2 * (p0 + pc);
+      if constexpr (NP > 8) {
+        ok = ok && (pc >= np || ((e0 >= n || buf[k].y == ep) && (e0 + 1 >= n || buf[k].w == ep)));
+      } else {
+        const bool cur = ((e0 >= n) | (buf[k].y == ep)) & ((e0 + 1 >= n) | (buf[k].w == ep));
+        ok = ok & ((pc >= np) | cur);
+      }
     }
 #if STAMD_POLL_STAMPS
     if (c.pph >= 0 && c.lane == 0) {
@@ -196,9 +205,10 @@ __device__ __forceinline__ bool pieces_current(const uint4 (&buf)[NP], int lane,
   bool ok = true;
 #pragma unroll
   for (int k = 0; k < NP; k++) {
-    int pc = lane + 64 * k;
-    int e0 = 2 * (p0 + pc);
-    ok = ok && (pc >= np || ((e0 >= n || buf[k].y == ep) && (e0 + 1 >= n || buf[k].w == ep)));
+    const int pc = lane + 64 * k;
+    const int e0 = 2 * (p0 + pc);
+    const bool cur = ((e0 >= n) | (buf[k].y == ep)) & ((e0 + 1 >= n) | (buf[k].w == ep));
+    ok = ok & ((pc >= np) | cur);
   }
   return ok;
 }
@@ -321,10 +331,13 @@ __device__ __forceinline__ void stage_vector(Ctx<P>& c, uint32_t tv, int n, int 
     x[k] = pc < np ? piece_values(buf[k], 2 * pc, n) : make_float2(0.f, 0.f);
     sum += x[k].x * x[k].x + x[k].y * x[k].y;
   }
+  // Every lane stores all kStageNP pieces (zeros past np): 2 * 64 * kStageNP = kMaxDim floats,
+  // within both the raw copy and the activation buffer, and past the vector's padded length,
+  // where no matvec reads. A store guarded per piece cost one divergent branch each.
+  static_assert(2 * 64 * kStageNP <= kMaxDim && kMaxDim <= kXs, "staged pieces fit the LDS buffers");
   if (raw) {
 #pragma unroll
-    for (int k = 0; k < kStageNP; k++)
-      if (c.lane + 64 * k < np) lds_store2(raw + 2 * (c.lane + 64 * k), x[k]);
+    for (int k = 0; k < kStageNP; k++) lds_store2(raw + 2 * (c.lane + 64 * k), x[k]);
   }
   if (norm) {
     const float scale = 1.0f / sqrtf(wave_total(sum) / (float)c.a.width + c.a.epsilon);
@@ -332,8 +345,7 @@ __device__ __forceinline__ void stage_vector(Ctx<P>& c, uint32_t tv, int n, int 
     for (int k = 0; k < kStageNP; k++) x[k] = make_float2(cast<P>(x[k].x * scale * w[k].x), cast<P>(x[k].y * scale * w[k].y));
   }
 #pragma unroll
-  for (int k = 0; k < kStageNP; k++)
-    if (c.lane + 64 * k < np) lds_store2(xs + 2 * (c.lane + 64 * k), x[k]);
+  for (int k = 0; k < kStageNP; k++) lds_store2(xs + 2 * (c.lane + 64 * k), x[k]);
 }
 
 // Units of a matvec phase owned by workgroup g: [first, first + count).
