@@ -199,43 +199,34 @@ __device__ __forceinline__ void poll_regs(Ctx<P>& c, uint32_t tv, int n, int p0,
 #endif
 }
 
-// True when every piece this lane holds (pieces below np) carries epoch ep.
-template <int NP>
-__device__ __forceinline__ bool pieces_current(const uint4 (&buf)[NP], int lane, int n, int p0, int np, unsigned ep) {
-  bool ok = true;
-#pragma unroll
-  for (int k = 0; k < NP; k++) {
-    const int pc = lane + 64 * k;
-    const int e0 = 2 * (p0 + pc);
-    const bool cur = ((e0 >= n) | (buf[k].y == ep)) & ((e0 + 1 >= n) | (buf[k].w == ep));
-    ok = ok & ((pc >= np) | cur);
-  }
-  return ok;
-}
-
 // Value pair of piece k (0 for padding at or beyond n).
 __device__ __forceinline__ float2 piece_values(uint4 b, int e0, int n) {
   return make_float2(e0 < n ? __builtin_bit_cast(float, b.x) : 0.f, e0 + 1 < n ? __builtin_bit_cast(float, b.z) : 0.f);
 }
 
-// poll_regs, then write the values (0 for padding) to dst[0 ..) in LDS.
-template <int P, int NP>
+// poll_regs, then write the values (0 for padding) to dst[0 ..) in LDS. With kAll every lane
+// stores all NP pieces (zeros past np): no divergent branch per piece, for callers whose
+// destination has room for 64 NP pieces.
+template <int P, int NP, bool kAll = false>
 __device__ __forceinline__ void poll_pieces(Ctx<P>& c, uint32_t tv, int n, int p0, int np, unsigned ep, float* dst) {
   uint4 buf[NP];
   poll_regs<P, NP>(c, tv, n, p0, np, ep, buf);
 #pragma unroll
   for (int k = 0; k < NP; k++) {
     int pc = c.lane + 64 * k;
-    if (pc < np) lds_store2(dst + 2 * pc, piece_values(buf[k], 2 * (p0 + pc), n));
+    if (kAll || pc < np) lds_store2(dst + 2 * pc, piece_values(buf[k], 2 * (p0 + pc), n));
   }
 }
 
-// Chunks first, first + step, ... of 1024 pieces of a wide vector into dst.
+// Chunks first, first + step, ... of 1024 pieces of a wide vector into the activation buffer
+// dst. The FFN width is at most 4096 (Runtime's config check), so a vector has at most two
+// chunks and a whole-chunk store ends at float 4096, inside the buffer.
 template <int P>
 __device__ __forceinline__ void poll_chunks(Ctx<P>& c, uint32_t tv, int n, int pieces, int first, int step, unsigned ep,
                                             float* dst) {
+  static_assert(2 * (1024 + 1024) <= kXs, "two whole 1024-piece chunks fit the activation buffer");
   for (int p0 = first * 1024; p0 < pieces; p0 += step * 1024)
-    poll_pieces<P, 16>(c, tv, n, p0, pieces - p0 < 1024 ? pieces - p0 : 1024, ep, dst + 2 * p0);
+    poll_pieces<P, 16, true>(c, tv, n, p0, pieces - p0 < 1024 ? pieces - p0 : 1024, ep, dst + 2 * p0);
 }
 
 // Whole vector of n elements padded to n_p (a multiple of 256) into dst[0 .. n_p). With
