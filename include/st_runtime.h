@@ -59,15 +59,25 @@ typedef struct {
   float epsilon;
 } st_config;
 
-/* = Stream::RuntimeOptions (include/Runtime.hpp:8-19) plus weight_dtype.
+/* = Stream::RuntimeOptions (include/Runtime.hpp:8-19) plus weight_dtype and initial_epoch.
  * blocks: workgroups of 512 threads; 0 selects one per compute unit.
+ * mapped (src/cuda/Runtime.cu:43-48,278-280,435-450): CUDA, GRAPH, FUSED and the CUBLAS
+ * backends read the event from, and write the score to, coherent host memory mapped into
+ * the device (a staging kernel before and after the step; inside the captured graph for
+ * GRAPH and CUBLAS_GRAPH) instead of pinned copies. The persistent worker always uses
+ * mapped memory.
  * vector_matvec and fused_attention are accepted for source compatibility; this
- * backend always uses its wide-load matvec and LDS-staged attention.
+ * backend always uses its wide-load matvec and its own windowed attention.
  * PERSISTENT only: backoff makes the worker and the host spin sleep between polls;
  * max_events > 0 ends the worker after that many RUN commands (RESET does not count);
  * initial_sequence is the mailbox's first sequence ID (the last ID is kept for STOP, so
  * values >= UINT64_MAX - 1 are rejected); idle_seconds ends a worker that receives no
- * command for that long. A call after the worker has ended fails with ST_ERR_STATE. */
+ * command for that long. A call after the worker has ended fails with ST_ERR_STATE.
+ * initial_epoch (extension, no counterpart in the reference): the first 32-bit epoch of the
+ * device's tagged dataflow (0 selects 1). Epochs advance by 5*layers+3 per step; before they
+ * would pass 0xF0000000 the runtime drains the device, zeroes the tagged vectors and restarts
+ * at 1 (a persistent worker is stopped and relaunched for this). Only tests set it, to start
+ * near that limit. */
 typedef struct {
   int32_t backend;
   int32_t blocks;
@@ -79,7 +89,7 @@ typedef struct {
   uint64_t initial_sequence;
   double idle_seconds;
   int32_t weight_dtype;
-  int32_t reserved;
+  uint32_t initial_epoch;
 } st_options;
 
 /* One named host tensor, FP32 values, row-major [out, in]. Names and shapes follow the

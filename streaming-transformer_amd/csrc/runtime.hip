@@ -171,8 +171,17 @@ static std::string probe_json() {
   HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device));
   char bus[64] = {0};
   (void)hipDeviceGetPCIBusId(bus, sizeof(bus), device);
+  // Some driver stacks report an empty marketing name; fall back to the ISA and CU count.
+  std::string name = p.name;
+  if (name.empty()) {
+    char buf[256] = {0};
+    if (hipDeviceGetName(buf, sizeof(buf), device) == hipSuccess) name = buf;
+  }
+  if (name.empty())
+    name = std::string("AMD ") + std::string(p.gcnArchName).substr(0, std::string(p.gcnArchName).find(':')) + " (" +
+           std::to_string(p.multiProcessorCount) + " CUs)";
   std::ostringstream o;
-  o << "{\"gpu\": \"" << json_escape(p.name) << "\", \"arch\": \"" << json_escape(p.gcnArchName)
+  o << "{\"gpu\": \"" << json_escape(name) << "\", \"arch\": \"" << json_escape(p.gcnArchName)
     << "\", \"device\": " << device << ", \"compute_units\": " << p.multiProcessorCount
     << ", \"lds_bytes_per_block\": " << p.sharedMemPerBlock
     << ", \"global_bytes\": " << p.totalGlobalMem << ", \"l2_bytes\": " << p.l2CacheSize
@@ -212,9 +221,19 @@ class Runtime {
 
  private:
   void build_weights(const st_tensor* tensors, size_t count);
+  // One step on the stream: the captured graph for GRAPH / CUBLAS_GRAPH (which holds the
+  // mapped staging kernels when `mapped`), else the backend's launches.
   void launch_step();
+  // One step's compute launches without the graph and without mapped staging.
+  void launch_compute();
   void launch_phases();
   void launch_fused(const float* event = nullptr);
+  // Epochs of the tagged dataflow: `steps` steps are about to run. Rebases first when they
+  // would pass kEpochLimit.
+  void reserve_epochs(uint64_t steps);
+  void rebase_epochs();
+  unsigned per_step() const { return 5u * (unsigned)c_.layers + 3u; }
+  bool tagged_steps() const { return !vendor(); }
   template <int P, int A> void launch_phases_t();
   template <int P, int A> void launch_fused_t(const float* event);
   template <int P, int A> void launch_trace_t(const float* events, int count, unsigned long long* stamps);
@@ -245,20 +264,32 @@ class Runtime {
   void reset_device();
   void start_worker();
   void command(int cmd);
+  void issue(int cmd);            // one mailbox round trip
+  void restart_worker_rebased();  // stop the worker, rebase the epochs, relaunch it
+  void stage_input();             // mapped: event from host-mapped memory into the device copy
+  void stage_output();            // mapped: score and error bits into host-mapped memory
   Mailbox* mailbox() { return reinterpret_cast<Mailbox*>(mailbox_.ptr); }
+
+  // Epochs stay below this bound, so the never-matching tag 0 and the all-ones sentinel of the
+  // workgroup-local flags are never live epochs.
+  static constexpr uint64_t kEpochLimit = 0xF0000000ull;
 
   st_config c_;
   st_options opt_;
   int prec_ = kFp32;
   int dim_ = 0, grid_ = 1, legal_blocks_ = 1, cus_ = 1, wall_khz_ = 100000;
+  int phase_grid_ = 1;       // workgroups of a phase launch (staged sequence)
+  bool phase_coop_ = false;  // phase launches are cooperative (the plain grid failed the probe)
   bool running_ = true;
   hipStream_t stream_ = nullptr;
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t graph_exec_ = nullptr;
-  DeviceBuffer weights_, keys_, values_, scratch_, tagged_, position_, epoch_, rope_, args_dev_;
+  DeviceBuffer weights_, keys_, values_, scratch_, tagged_, position_, epoch_dev_, rope_, args_dev_;
   PinnedBuffer host_in_, host_out_;
-  MappedBuffer mailbox_, mapped_in_, mapped_snap_;
+  MappedBuffer mailbox_, mapped_in_, mapped_snap_, mapped_io_;
   uint64_t sequence_ = 0;
+  uint64_t epoch_ = 1;       // host copy of the device epoch (the next step's phase-0 epoch)
+  uint64_t runs_done_ = 0;   // RUN commands the persistent worker has completed
   hipStream_t copy_stream_ = nullptr;
   StepArgs args_{};
   const StepArgs* dargs_ = nullptr;
@@ -384,11 +415,12 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   position_.alloc(8);
   HIP_CHECK(hipMemset(position_.ptr, 0, 8));
   a.position = reinterpret_cast<unsigned long long*>(position_.ptr);
-  epoch_.alloc(64);
-  const unsigned first_epoch = 1;
-  HIP_CHECK(hipMemset(epoch_.ptr, 0, 64));
-  HIP_CHECK(hipMemcpy(epoch_.ptr, &first_epoch, 4, hipMemcpyHostToDevice));
-  a.epoch = reinterpret_cast<unsigned*>(epoch_.ptr);
+  epoch_dev_.alloc(64);
+  epoch_ = options.initial_epoch ? options.initial_epoch : 1u;
+  const unsigned first_epoch = (unsigned)epoch_;
+  HIP_CHECK(hipMemset(epoch_dev_.ptr, 0, 64));
+  HIP_CHECK(hipMemcpy(epoch_dev_.ptr, &first_epoch, 4, hipMemcpyHostToDevice));
+  a.epoch = reinterpret_cast<unsigned*>(epoch_dev_.ptr);
 
   // RoPE inverse frequencies: powf(10000, -i/dim) for even i (src/cpu/Cpu.cpp:75).
   std::vector<float> freq(dim_ / 2);
@@ -401,6 +433,10 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   host_in_.alloc((size_t)a.features_p * 4);
   std::memset(host_in_.ptr, 0, (size_t)a.features_p * 4);
   host_out_.alloc(64);
+  if (options.mapped && options.backend != ST_BACKEND_PERSISTENT) {
+    // The event (features_p floats, zero padding) followed by the score and the error word.
+    mapped_io_.alloc((size_t)a.features_p * 4 + 64);
+  }
 
   // ---- grid
   legal_blocks_ = dispatch([&](auto P, auto A) { return legal_blocks_t<P.value, A.value>(); });
@@ -410,6 +446,7 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
     throw Error(ST_ERR_INVALID,
                 "Requested cooperative grid exceeds actual occupancy limit " + std::to_string(legal_blocks_));
   a.grid = grid_;
+  phase_grid_ = std::min(grid_, legal_blocks_);
   if (options.backend == ST_BACKEND_PERSISTENT) {
     mailbox_.alloc(sizeof(Mailbox));
     mapped_in_.alloc((size_t)c_.features * 4);
@@ -440,39 +477,48 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   dargs_ = reinterpret_cast<const StepArgs*>(args_dev_.ptr);
 
   reset_device();
-  if (vendor()) {
-    vendor_ = std::make_unique<VendorPath>(c_, prec_ == kMixed, args_, tensors, count, stream_);
-    if (options.backend == ST_BACKEND_CUBLAS_GRAPH) {
-      // Warm the library outside capture, restore the initial state, then capture.
-      vendor_->launch();
-      sync();
-      reset_device();
-      HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
-      vendor_->launch();
-      HIP_CHECK(hipStreamEndCapture(stream_, &graph_));
-      HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
-    }
+  if (options.backend == ST_BACKEND_CUDA && phase_grid_ > 1 && !coresident(phase_grid_)) {
+    // Phase launches exchange data within the launch, so their workgroups must be resident
+    // together: when a plain launch of this grid is not, launch the phases cooperatively.
+    phase_coop_ = true;
   }
-  if (options.backend == ST_BACKEND_GRAPH) {
-    // The graph holds one step: the fused kernel as a single plain node when the grid is
-    // resident all at once (bit-identical to the phase sequence), else the phase sequence.
-    // Warm up outside capture, restore the initial state, then capture.
-    graph_fused_ = grid_ > 1 && grid_ <= legal_blocks_ && coresident(grid_);
-    if (graph_fused_) plain_launch_ = true;
-    auto sequence = [&] {
-      if (graph_fused_) launch_fused();
-      else launch_phases();
-    };
+  // The captured graph holds one step, with the mapped staging kernels around it (the
+  // reference captures stage_input and stage_output with the sequence, src/cuda/Runtime.cu:
+  // 276-283). Warm up outside capture, restore the initial state, then capture.
+  auto capture = [&](auto&& sequence) {
+    if (tagged_steps()) reserve_epochs(1);
     sequence();
     sync();
     reset_device();
     HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    if (opt_.mapped) stage_input();
     sequence();
+    if (opt_.mapped) stage_output();
     HIP_CHECK(hipStreamEndCapture(stream_, &graph_));
     HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+  };
+  if (vendor()) {
+    vendor_ = std::make_unique<VendorPath>(c_, prec_ == kMixed, args_, tensors, count, stream_);
+    if (options.backend == ST_BACKEND_CUBLAS_GRAPH) capture([&] { vendor_->launch(); });
+  }
+  if (options.backend == ST_BACKEND_GRAPH) {
+    // The graph holds the fused kernel as a single plain node when the grid is resident all
+    // at once (bit-identical to the phase sequence), else the phase sequence, on the largest
+    // grid (halving from the requested one) that a plain launch keeps resident: captured
+    // launches cannot be cooperative.
+    graph_fused_ = grid_ > 1 && grid_ <= legal_blocks_ && coresident(grid_);
+    if (graph_fused_) plain_launch_ = true;
+    while (!graph_fused_ && phase_grid_ > 1 && !coresident(phase_grid_)) phase_grid_ /= 2;
+    capture([&] {
+      if (graph_fused_) launch_fused();
+      else launch_phases();
+    });
   }
   if (options.backend == ST_BACKEND_FUSED && grid_ > 1) plain_launch_ = coresident(grid_);
-  if (persistent()) start_worker();
+  if (persistent()) {
+    if (epoch_ + 2ull * per_step() > kEpochLimit) rebase_epochs();
+    start_worker();
+  }
 }
 
 // Co-residency probe: one plain launch of `grid` workgroups with the fused kernel's footprint
@@ -527,11 +573,12 @@ Runtime::~Runtime() {
 
 template <int P, int A>
 int Runtime::legal_blocks_t() {
-  int per_cu = 0;
+  int per_cu = 0, trace_per_cu = 0, phase_per_cu = 0, worker_per_cu = 0;
   HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_kernel<P, A>, kThreads, 0));
-  int trace_per_cu = 0;
   HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&trace_per_cu, trace_kernel<P, A>, kThreads, 0));
-  return std::max(1, std::min(per_cu, trace_per_cu) * cus_);
+  HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&phase_per_cu, phase_kernel<P, A>, kThreads, 0));
+  HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&worker_per_cu, persistent_kernel<P, A>, kThreads, 0));
+  return std::max(1, std::min({per_cu, trace_per_cu, phase_per_cu, worker_per_cu}) * cus_);
 }
 
 // Weight arena in phase order: input, then per layer norm1, norm2, qkv (stacked q;k;v),
@@ -645,11 +692,18 @@ template <int P, int A>
 void Runtime::launch_phases_t() {
   const int nph = 5 * c_.layers + 2;
   // Attention chunks of one head are combined by polling partials written in the same
-  // launch, so every workgroup of a launch must be resident at once.
-  const int resident = std::min(grid_, legal_blocks_);
+  // launch, so every workgroup of a launch must be resident at once: phase_grid_ passed the
+  // co-residency probe, or the launches are cooperative.
   for (int ph = 0; ph < nph; ph++) {
-    int grid = ph == nph - 1 ? 1 : resident;
-    hipLaunchKernelGGL((phase_kernel<P, A>), dim3(grid), dim3(kThreads), 0, stream_, dargs_, ph);
+    int grid = ph == nph - 1 ? 1 : phase_grid_;
+    if (phase_coop_ && grid > 1) {
+      const StepArgs* args = dargs_;
+      void* params[] = {&args, &ph};
+      HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<void*>(phase_kernel<P, A>), dim3(grid), dim3(kThreads),
+                                           params, 0, stream_));
+    } else {
+      hipLaunchKernelGGL((phase_kernel<P, A>), dim3(grid), dim3(kThreads), 0, stream_, dargs_, ph);
+    }
   }
   HIP_CHECK(hipGetLastError());
 }
@@ -676,11 +730,58 @@ void Runtime::launch_fused(const float* event) {
 }
 
 void Runtime::launch_step() {
-  if (opt_.backend == ST_BACKEND_GRAPH || opt_.backend == ST_BACKEND_CUBLAS_GRAPH)
+  if (opt_.backend == ST_BACKEND_GRAPH || opt_.backend == ST_BACKEND_CUBLAS_GRAPH) {
     HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
-  else if (opt_.backend == ST_BACKEND_FUSED) launch_fused();
-  else if (opt_.backend == ST_BACKEND_CUBLAS) vendor_->launch();
+    return;
+  }
+  if (opt_.mapped) stage_input();
+  launch_compute();
+  if (opt_.mapped) stage_output();
+}
+
+void Runtime::launch_compute() {
+  if (opt_.backend == ST_BACKEND_FUSED || (opt_.backend == ST_BACKEND_GRAPH && graph_fused_)) launch_fused();
+  else if (vendor()) vendor_->launch();
   else launch_phases();
+}
+
+// Mapped staging kernels (the reference's stage_input / stage_output, src/cuda/Runtime.cu:
+// 43-48): the event is read from host memory mapped into the device, the score and the
+// error word are written back there.
+__global__ void stage_input_kernel(const float* mapped, float* input, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) input[i] = mapped[i];
+}
+__global__ void stage_output_kernel(const float* score_and_error, float* mapped) {
+  if (threadIdx.x < 2) mapped[threadIdx.x] = score_and_error[threadIdx.x];
+}
+
+void Runtime::stage_input() {
+  hipLaunchKernelGGL(stage_input_kernel, dim3(1), dim3(256), 0, stream_, reinterpret_cast<const float*>(mapped_io_.dev),
+                     args_.scratch + args_.s_input, args_.features_p);
+  HIP_CHECK(hipGetLastError());
+}
+
+void Runtime::stage_output() {
+  hipLaunchKernelGGL(stage_output_kernel, dim3(1), dim3(64), 0, stream_, args_.scratch + args_.s_score,
+                     reinterpret_cast<float*>(mapped_io_.dev) + args_.features_p);
+  HIP_CHECK(hipGetLastError());
+}
+
+void Runtime::rebase_epochs() {
+  // Drain the device, zero every tag (tag 0 never matches a live epoch), restart at 1.
+  sync();
+  HIP_CHECK(hipMemsetAsync(tagged_.ptr, 0, args_.tagged_bytes, stream_));
+  const unsigned one = 1;
+  HIP_CHECK(hipMemcpyAsync(epoch_dev_.ptr, &one, 4, hipMemcpyHostToDevice, stream_));
+  sync();
+  epoch_ = 1;
+}
+
+void Runtime::reserve_epochs(uint64_t steps) {
+  const uint64_t need = steps * per_step();
+  if (need >= kEpochLimit) throw Error(ST_ERR_INVALID, "Too many steps in one launch for the 32-bit epoch range");
+  if (epoch_ + need > kEpochLimit) rebase_epochs();
+  epoch_ += need;
 }
 
 void Runtime::check_device_error() {
@@ -697,13 +798,22 @@ float Runtime::step(const float* input) {
     command(kCmdRun);
     return mailbox()->score;
   }
-  std::memcpy(host_in_.ptr, input, (size_t)c_.features * 4);
-  HIP_CHECK(hipMemcpyAsync(args_.scratch + args_.s_input, host_in_.ptr, (size_t)args_.features_p * 4,
-                           hipMemcpyHostToDevice, stream_));
-  launch_step();
-  HIP_CHECK(hipMemcpyAsync(host_out_.ptr, args_.scratch + args_.s_score, 8, hipMemcpyDeviceToHost, stream_));
-  sync();
-  const float* out = reinterpret_cast<const float*>(host_out_.ptr);
+  if (tagged_steps()) reserve_epochs(1);
+  const float* out;
+  if (opt_.mapped) {
+    std::memcpy(mapped_io_.ptr, input, (size_t)c_.features * 4);
+    launch_step();  // staging kernels included
+    sync();
+    out = reinterpret_cast<const float*>(mapped_io_.ptr) + args_.features_p;
+  } else {
+    std::memcpy(host_in_.ptr, input, (size_t)c_.features * 4);
+    HIP_CHECK(hipMemcpyAsync(args_.scratch + args_.s_input, host_in_.ptr, (size_t)args_.features_p * 4,
+                             hipMemcpyHostToDevice, stream_));
+    launch_step();
+    HIP_CHECK(hipMemcpyAsync(host_out_.ptr, args_.scratch + args_.s_score, 8, hipMemcpyDeviceToHost, stream_));
+    sync();
+    out = reinterpret_cast<const float*>(host_out_.ptr);
+  }
   unsigned err;
   std::memcpy(&err, out + 1, 4);
   if (err) throw Error(ST_ERR_NUMERIC, "Device watchdog tripped (error bits " + std::to_string(err) + ")");
@@ -750,10 +860,24 @@ void Runtime::start_worker() {
   });
 }
 
+// The worker's epochs would pass kEpochLimit: stop it (a STOP round trip; the runtime stays
+// running), rebase, and relaunch it continuing the mailbox sequence and the RUN budget. The
+// device state (K/V, hidden, position) is untouched.
+void Runtime::restart_worker_rebased() {
+  issue(kCmdStop);
+  sync();
+  rebase_epochs();
+  mailbox()->exited = 0;
+  args_.initial_sequence = sequence_;
+  args_.max_events = opt_.max_events ? opt_.max_events - runs_done_ : 0;
+  HIP_CHECK(hipMemcpy(args_dev_.ptr, &args_, sizeof(StepArgs), hipMemcpyHostToDevice));
+  start_worker();
+}
+
 // One command through the mailbox (src/cuda/Runtime.cu:398-428, docs/transport.md:9-16): the
 // input and command are written before the request word is released; the worker's
 // completion word is acquired before the score is read. The last sequence ID is kept for
-// STOP.
+// STOP. Every command uses one step's worth of epochs.
 void Runtime::command(int cmd) {
   if (!running_) throw Error(ST_ERR_STATE, "Persistent runtime is stopped");
   Mailbox* mb = mailbox();
@@ -765,6 +889,16 @@ void Runtime::command(int cmd) {
     running_ = false;
     throw Error(ST_ERR_STATE, "Persistent worker exited: finite-event or idle budget reached");
   }
+  // Room for this command and a later STOP; the rebase itself uses one STOP's worth.
+  if (cmd != kCmdStop && epoch_ + 2ull * per_step() > kEpochLimit && sequence_ + 2 < maximum)
+    restart_worker_rebased();
+  issue(cmd);
+  if (cmd == kCmdRun) runs_done_++;
+}
+
+void Runtime::issue(int cmd) {
+  Mailbox* mb = mailbox();
+  epoch_ += per_step();
   mb->command = cmd;
   __atomic_store_n(&mb->request, ++sequence_, __ATOMIC_RELEASE);
   const auto start = std::chrono::steady_clock::now();
@@ -858,6 +992,7 @@ double Runtime::device_trace(const float* inputs, size_t count, double* per_even
   trace.alloc(padded.size() * 4);
   HIP_CHECK(hipMemcpy(trace.ptr, padded.data(), padded.size() * 4, hipMemcpyHostToDevice));
   reset();
+  if (tagged_steps()) reserve_epochs(count);
   std::vector<double> durations(count);
   double mean = 0;
   if (opt_.backend == ST_BACKEND_FUSED) {
@@ -878,7 +1013,10 @@ double Runtime::device_trace(const float* inputs, size_t count, double* per_even
     for (size_t i = 0; i < count; i++) {
       HIP_CHECK(hipMemcpyAsync(args_.scratch + args_.s_input, reinterpret_cast<float*>(trace.ptr) + i * fp,
                                (size_t)fp * 4, hipMemcpyDeviceToDevice, stream_));
-      launch_step();
+      // A mapped graph stages host I/O inside the capture: run the compute launches instead
+      // (the reference does the same, src/cuda/Runtime.cu:617-622).
+      if (opt_.mapped) launch_compute();
+      else launch_step();
       HIP_CHECK(hipEventRecord(ev[i + 1], stream_));
     }
     sync();
@@ -914,6 +1052,7 @@ double Runtime::device_run(const float* inputs, size_t count, bool reset_first, 
   trace.alloc(padded.size() * 4);
   HIP_CHECK(hipMemcpy(trace.ptr, padded.data(), padded.size() * 4, hipMemcpyHostToDevice));
   if (reset_first) reset();
+  if (tagged_steps()) reserve_epochs(count);
   std::vector<hipEvent_t> ev(count + 1);
   for (auto& e : ev) HIP_CHECK(hipEventCreate(&e));
   const float* base = reinterpret_cast<const float*>(trace.ptr);
@@ -924,7 +1063,8 @@ double Runtime::device_run(const float* inputs, size_t count, bool reset_first, 
     } else {
       HIP_CHECK(hipMemcpyAsync(args_.scratch + args_.s_input, base + i * fp, (size_t)fp * 4,
                                hipMemcpyDeviceToDevice, stream_));
-      launch_step();
+      if (opt_.mapped) launch_compute();
+      else launch_step();
     }
     HIP_CHECK(hipEventRecord(ev[i + 1], stream_));
   }
@@ -1085,9 +1225,15 @@ std::vector<std::pair<std::string, std::vector<float>>> Runtime::trace_step(cons
   };
   auto run_phase = [&](int ph) {
     dispatch([&](auto P, auto A) {
-      const int resident = std::min(grid_, legal_blocks_);
-      const int grid = ph == 5 * c_.layers + 1 ? 1 : resident;
-      hipLaunchKernelGGL((phase_kernel<P.value, A.value>), dim3(grid), dim3(kThreads), 0, stream_, dargs_, ph);
+      const int grid = ph == 5 * c_.layers + 1 ? 1 : phase_grid_;
+      if (phase_coop_ && grid > 1) {
+        const StepArgs* args = dargs_;
+        void* params[] = {&args, &ph};
+        HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<void*>(phase_kernel<P.value, A.value>), dim3(grid),
+                                             dim3(kThreads), params, 0, stream_));
+      } else {
+        hipLaunchKernelGGL((phase_kernel<P.value, A.value>), dim3(grid), dim3(kThreads), 0, stream_, dargs_, ph);
+      }
       return 0;
     });
     HIP_CHECK(hipGetLastError());
@@ -1124,6 +1270,7 @@ std::vector<std::pair<std::string, std::vector<float>>> Runtime::trace_step(cons
     return t[n + ".norm"];
   };
 
+  reserve_epochs(1);
   std::memcpy(host_in_.ptr, input, (size_t)f * 4);
   HIP_CHECK(hipMemcpyAsync(a.scratch + a.s_input, host_in_.ptr, (size_t)a.features_p * 4, hipMemcpyHostToDevice,
                            stream_));
@@ -1193,6 +1340,7 @@ size_t Runtime::phase_times(const float* input, double* us, size_t cap) {
   prof.stamps = reinterpret_cast<unsigned long long*>(stamps.ptr);
   args.alloc(sizeof(StepArgs));
   HIP_CHECK(hipMemcpy(args.ptr, &prof, sizeof(StepArgs), hipMemcpyHostToDevice));
+  reserve_epochs(1);
   std::memcpy(host_in_.ptr, input, (size_t)c_.features * 4);
   HIP_CHECK(hipMemcpyAsync(args_.scratch + args_.s_input, host_in_.ptr, (size_t)args_.features_p * 4,
                            hipMemcpyHostToDevice, stream_));
@@ -1242,7 +1390,11 @@ std::string Runtime::info() {
     << ", \"matvec_implementation\": \"wave64 16-byte buffer loads, register ring, butterfly reduction\""
     << ", \"attention_implementation\": \"" << (args_.attn_regs ? "register" : "LDS-staged")
     << " window chunks, tagged partials combined by the chunk-0 wave\""
-    << ", \"transport\": \"" << (worker ? "mapped-mailbox-persistent-worker" : "pinned-copy-stream-sync") << "\""
+    << ", \"transport\": \""
+    << (worker ? "mapped-system-load-store" : opt_.mapped ? "mapped-stream-sync" : "pinned-copy-stream-sync") << "\""
+    << ", \"poll_policy\": \"" << (opt_.backoff ? "bounded-device-backoff-host-yield" : "tight") << "\""
+    << ", \"workspace_storage\": \"FP32 with explicit FP16 rounding in mixed mode\""
+    << ", \"phase_launch\": \"" << (phase_coop_ ? "cooperative" : "plain") << "\", \"phase_blocks\": " << phase_grid_
     << ", \"weights_and_kv_storage\": \""
     << (prec_ == kMixed ? "FP16/FP16" : prec_ == kBf16w ? "BF16/FP32" : "FP32/FP32") << "\"}";
   return o.str();
@@ -1458,9 +1610,11 @@ std::string transport_bench(const std::string& mode, uint64_t count, bool backof
   if (csv_path && *csv_path) {
     FILE* f = std::fopen(csv_path, "w");
     if (!f) throw Error(ST_ERR_INVALID, std::string("Cannot write ") + csv_path);
-    std::fprintf(f, "sequence,host_observation_us,device_round_trip_or_wait_us\n");
+    // The reference's columns (src/cuda/Runtime.cu:803-805). The device column counts ticks of
+    // the constant wall clock (its rate is "wall_clock_khz" of the environment report).
+    std::fprintf(f, "sequence,host_observation_us,device_round_trip_or_wait_cycles\n");
     for (uint64_t i = 0; i < count; i++)
-      std::fprintf(f, "%llu,%.17g,%.17g\n", (unsigned long long)(i + 1), samples[i], ticks[i] * 1000.0 / wall_khz);
+      std::fprintf(f, "%llu,%.17g,%llu\n", (unsigned long long)(i + 1), samples[i], (unsigned long long)ticks[i]);
     std::fclose(f);
   }
   std::vector<double> sorted = samples;

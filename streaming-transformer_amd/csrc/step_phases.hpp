@@ -539,6 +539,10 @@ struct AttnWork {
   __device__ __forceinline__ uint32_t partial(int h, int ch) const { return (uint32_t)(h * nch + ch); }
 };
 
+// Workgroup that computes attention item `it` (every layer): item it goes to wave wid = it mod
+// nw, and wid = g + grid * sw, so the workgroup is it mod grid.
+__device__ __forceinline__ int attn_item_workgroup(int it, int grid) { return it % grid; }
+
 template <int P>
 __device__ __forceinline__ AttnWork attn_work(const StepArgs& a, int grid, int g, int sw) {
   AttnWork w;
@@ -1385,16 +1389,18 @@ __global__ __launch_bounds__(kThreads) void trace_kernel(const StepArgs* __restr
 }
 
 // Persistent worker's RESET: this workgroup zeroes, with write-through stores, the K/V rows
-// of the attention chunks it reads (items it with it % grid == g, in every layer), so no
-// other XCD's L2 holds a stale copy of them; a grid-strided share of the hidden state; and
-// (workgroup 0) the position.
+// of the attention items it computes (attn_item_workgroup, decoded like AttnWork: chunk-major),
+// in every layer, so the only L2 that can hold those rows is its own; a grid-strided share of
+// the hidden state; and (workgroup 0) the position.
 template <int P>
 __device__ __forceinline__ void reset_owned(Ctx<P>& c) {
   const StepArgs& a = c.a;
-  const int nch = (a.window + a.chunk - 1) / a.chunk;
-  const int total = a.heads * nch;
+  const AttnWork w = attn_work<P>(a, c.grid, c.g, 0);
+  const int total = a.heads * w.nch;
   for (int it = c.g; it < total; it += c.grid) {
-    const int h = it / nch, ch = it - h * nch;
+    if (attn_item_workgroup(it, c.grid) != c.g) continue;
+    int h, ch;
+    w.decode(it, h, ch);
     const int row0 = ch * a.chunk;
     const int rows = a.window - row0 < a.chunk ? a.window - row0 : a.chunk;
     const uint32_t bytes = (uint32_t)rows * (uint32_t)a.dim * Traits<P>::kKvBytes;  // a multiple of 4
@@ -1421,7 +1427,7 @@ __host__ __device__ __forceinline__ uint32_t snapshot_ring_bytes(int layers, int
 
 // SNAPSHOT (persistent worker): copy the carried state into the host buffer while the worker
 // stays resident (copy commands on another queue cannot start while the worker holds every
-// CU). Each workgroup copies the ring chunks of the RESET split and a grid-strided share of the
+// CU). Each workgroup copies the ring chunks it computes (as RESET) and a grid-strided share of the
 // hidden state, all with coherent loads; workgroup 0 writes the position. The stores go to
 // fine-grained host memory; the worker releases them (system scope) before reporting done.
 template <int P>
@@ -1429,10 +1435,12 @@ __device__ __forceinline__ void snapshot_owned(Ctx<P>& c, unsigned long long t) 
   const StepArgs& a = c.a;
   unsigned char* out = a.mapped_snapshot;
   const uint32_t ring = snapshot_ring_bytes(a.layers, a.width, a.window, Traits<P>::kKvBytes);
-  const int nch = (a.window + a.chunk - 1) / a.chunk;
-  const int total = a.heads * nch;
+  const AttnWork w = attn_work<P>(a, c.grid, c.g, 0);
+  const int total = a.heads * w.nch;
   for (int it = c.g; it < total; it += c.grid) {
-    const int h = it / nch, ch = it - h * nch;
+    if (attn_item_workgroup(it, c.grid) != c.g) continue;
+    int h, ch;
+    w.decode(it, h, ch);
     const int row0 = ch * a.chunk;
     const int rows = a.window - row0 < a.chunk ? a.window - row0 : a.chunk;
     const uint32_t bytes = (uint32_t)rows * (uint32_t)a.dim * Traits<P>::kKvBytes;  // a multiple of 4

@@ -52,6 +52,7 @@ class RuntimeOptions:
     initial_sequence: int = 0
     idle_seconds: float = 30.0
     weight_dtype: WeightStorage = WeightStorage.AS_MODEL
+    initial_epoch: int = 0  # first epoch of the device's tagged dataflow (0 = 1); tests only
 
 
 class _Config(ctypes.Structure):
@@ -65,7 +66,7 @@ class _Options(ctypes.Structure):
                 ('mapped', ctypes.c_int32), ('vector_matvec', ctypes.c_int32),
                 ('fused_attention', ctypes.c_int32), ('max_events', ctypes.c_uint64),
                 ('initial_sequence', ctypes.c_uint64), ('idle_seconds', ctypes.c_double),
-                ('weight_dtype', ctypes.c_int32), ('reserved', ctypes.c_int32)]
+                ('weight_dtype', ctypes.c_int32), ('initial_epoch', ctypes.c_uint32)]
 
 
 class _Tensor(ctypes.Structure):
@@ -200,7 +201,7 @@ class Runtime:
         o = self.options
         opts = _Options(int(o.backend), int(o.blocks), int(o.backoff), int(o.mapped), int(o.vector_matvec),
                         int(o.fused_attention), int(o.max_events), int(o.initial_sequence),
-                        float(o.idle_seconds), int(o.weight_dtype), 0)
+                        float(o.idle_seconds), int(o.weight_dtype), int(o.initial_epoch))
         handle = ctypes.c_void_p()
         _check(lib.st_runtime_create(ctypes.byref(cfg), int(self.mixed), array, len(array), ctypes.byref(opts),
                                      ctypes.byref(handle)))

@@ -18,6 +18,6 @@ def test_transport_modes(tmp_path, mode, backoff):
     assert report['mode'] == mode and report['events'] == 300 and report['failed'] == 0
     assert 0 < report['p50_us'] <= report['p99_us'] <= report['worst_us']
     rows = list(csv.reader(out.open()))
-    assert rows[0] == ['sequence', 'host_observation_us', 'device_round_trip_or_wait_us'] and len(rows) == 301
+    assert rows[0] == ['sequence', 'host_observation_us', 'device_round_trip_or_wait_cycles'] and len(rows) == 301
     if mode in ('ping-pong', 'gpu-ping'):
         assert all(float(r[2]) > 0 for r in rows[1:])
