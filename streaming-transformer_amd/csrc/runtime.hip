@@ -20,6 +20,7 @@
 #include <limits>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <sstream>
 #include <stdexcept>
 #include <string>
@@ -195,6 +196,30 @@ static std::string probe_json() {
 
 // ---------------------------------------------------------------------------------------------
 
+// The allocation-free device trace. Stamps of the per-step wall clock go to a fixed device
+// array of kNoAllocMaxEvents + 1 entries (8 MiB per GPU, held until the process ends). In
+// host code the array's name only stands for the symbol: its device address on each GPU is
+// looked up once (hipGetSymbolAddress, with that device current) and kept per device.
+constexpr size_t kNoAllocMaxEvents = (size_t)1 << 20;
+static __device__ __align__(256) unsigned long long trace_scratch[kNoAllocMaxEvents + 1];
+
+static std::mutex g_scratch_mutex;
+static std::map<int, unsigned long long*> g_scratch_ptr;  // device -> address of trace_scratch there
+
+// Looks up (once per device) the address of trace_scratch on the current device.
+static unsigned long long* trace_scratch_address() {
+  int device = 0;
+  HIP_CHECK(hipGetDevice(&device));
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  auto it = g_scratch_ptr.find(device);
+  if (it != g_scratch_ptr.end()) return it->second;
+  void* ptr = nullptr;
+  HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(trace_scratch)));
+  if (!ptr) throw Error(ST_ERR_DEVICE, "No device address for the trace scratch array");
+  g_scratch_ptr[device] = reinterpret_cast<unsigned long long*>(ptr);
+  return g_scratch_ptr[device];
+}
+
 #include "vendor_path.hpp"
 
 class Runtime {
@@ -207,6 +232,9 @@ class Runtime {
   void stop();
   void snapshot(uint64_t* position, float* keys, float* values, float* hidden);
   double device_trace(const float* inputs, size_t count, double* per_event);
+  // deviceTrace without allocation: events already in device memory, stamps in the
+  // library's fixed device array.
+  double device_trace_noalloc(const float* device_events, size_t count, double* per_event);
   double device_run(const float* inputs, size_t count, bool reset_first, double* per_event);
   size_t phase_times(const float* input, double* us, size_t cap);
   // traceStep: names and sizes of the trace entries in output order (fixed by the config).
@@ -236,7 +264,7 @@ class Runtime {
   bool tagged_steps() const { return !vendor(); }
   template <int P, int A> void launch_phases_t();
   template <int P, int A> void launch_fused_t(const float* event);
-  template <int P, int A> void launch_trace_t(const float* events, int count, unsigned long long* stamps);
+  template <int P, int A> void launch_trace_t(const float* events, int count, int stride, unsigned long long* stamps);
   template <int P, int A> int legal_blocks_t();
   // Call f(precision, attention path) with both as integral constants.
   template <class F> auto dispatch(F&& f) {
@@ -289,6 +317,7 @@ class Runtime {
   MappedBuffer mailbox_, mapped_in_, mapped_snap_, mapped_io_;
   uint64_t sequence_ = 0;
   uint64_t epoch_ = 1;       // host copy of the device epoch (the next step's phase-0 epoch)
+  unsigned long long* scratch_ptr_ = nullptr;  // this device's trace_scratch (allocation-free trace)
   uint64_t runs_done_ = 0;   // RUN commands the persistent worker has completed
   hipStream_t copy_stream_ = nullptr;
   StepArgs args_{};
@@ -326,6 +355,7 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
     throw Error(ST_ERR_DEVICE, std::string("Supported target is gfx950; found ") + prop.gcnArchName);
   cus_ = prop.multiProcessorCount;
   HIP_CHECK(hipDeviceGetAttribute(&wall_khz_, hipDeviceAttributeWallClockRate, device));
+  scratch_ptr_ = trace_scratch_address();
   HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   HIP_CHECK(hipStreamCreateWithFlags(&copy_stream_, hipStreamNonBlocking));
 
@@ -967,11 +997,11 @@ void Runtime::snapshot(uint64_t* position, float* keys, float* values, float* hi
 }
 
 template <int P, int A>
-void Runtime::launch_trace_t(const float* events, int count, unsigned long long* stamps) {
+void Runtime::launch_trace_t(const float* events, int count, int stride, unsigned long long* stamps) {
   if (grid_ == 1) {
-    hipLaunchKernelGGL((trace_kernel<P, A>), dim3(1), dim3(kThreads), 0, stream_, dargs_, events, count, stamps);
+    hipLaunchKernelGGL((trace_kernel<P, A>), dim3(1), dim3(kThreads), 0, stream_, dargs_, events, count, stride, stamps);
   } else {
-    void* params[] = {&dargs_, &events, &count, &stamps};
+    void* params[] = {&dargs_, &events, &count, &stride, &stamps};
     HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<void*>(trace_kernel<P, A>), dim3(grid_),
                                          dim3(kThreads), params, 0, stream_));
   }
@@ -1000,7 +1030,7 @@ double Runtime::device_trace(const float* inputs, size_t count, double* per_even
     stamps.alloc((count + 1) * 8);
     const float* ev = reinterpret_cast<const float*>(trace.ptr);
     auto* st_ptr = (unsigned long long*)stamps.ptr;
-    dispatch([&](auto P, auto A) { launch_trace_t<P.value, A.value>(ev, (int)count, st_ptr); return 0; });
+    dispatch([&](auto P, auto A) { launch_trace_t<P.value, A.value>(ev, (int)count, fp, st_ptr); return 0; });
     sync();
     std::vector<unsigned long long> st(count + 1);
     HIP_CHECK(hipMemcpy(st.data(), stamps.ptr, st.size() * 8, hipMemcpyDeviceToHost));
@@ -1033,6 +1063,44 @@ double Runtime::device_trace(const float* inputs, size_t count, double* per_even
   check_device_error();
   if (per_event) std::copy(durations.begin(), durations.end(), per_event);
   return mean;
+}
+
+double Runtime::device_trace_noalloc(const float* device_events, size_t count, double* per_event) {
+  if (!running_) throw Error(ST_ERR_STATE, "Runtime is stopped");
+  if (opt_.backend != ST_BACKEND_FUSED)
+    throw Error(ST_ERR_INVALID, "The allocation-free device trace runs on the fused backend only");
+  if (!device_events || count == 0) throw Error(ST_ERR_INVALID, "Invalid trace (null or empty)");
+  if (count > kNoAllocMaxEvents)
+    throw Error(ST_ERR_INVALID, "Allocation-free device trace is limited to " + std::to_string(kNoAllocMaxEvents) +
+                                    " events per call (its stamp array is fixed)");
+  hipPointerAttribute_t attr{};
+  if (hipPointerGetAttributes(&attr, device_events) != hipSuccess) {
+    (void)hipGetLastError();  // an unknown pointer is an argument error, not a device one
+    throw Error(ST_ERR_INVALID, "Events must be in device memory");
+  }
+  if (attr.type != hipMemoryTypeDevice) throw Error(ST_ERR_INVALID, "Events must be in device memory");
+  unsigned long long* stamps = scratch_ptr_;
+  reset();
+  reserve_epochs(count);
+  const int stride = c_.features;
+  dispatch([&](auto P, auto A) { launch_trace_t<P.value, A.value>(device_events, (int)count, stride, stamps); return 0; });
+  sync();
+  check_device_error();
+  // Stamps 1..count land in per_event (as 64-bit words) and become durations in place, last
+  // first, so that stamp i is still unread when duration i is written.
+  unsigned long long first = 0, last = 0;
+  HIP_CHECK(hipMemcpy(&first, stamps, 8, hipMemcpyDeviceToHost));
+  HIP_CHECK(hipMemcpy(&last, stamps + count, 8, hipMemcpyDeviceToHost));
+  if (per_event) {
+    static_assert(sizeof(double) == sizeof(unsigned long long), "stamps and durations share storage");
+    HIP_CHECK(hipMemcpy(per_event, stamps + 1, count * 8, hipMemcpyDeviceToHost));
+    unsigned long long* words = reinterpret_cast<unsigned long long*>(per_event);
+    for (size_t i = count; i-- > 0;) {
+      const unsigned long long hi = words[i], lo = i ? words[i - 1] : first;
+      per_event[i] = (double)(hi - lo) * 1000.0 / wall_khz_;
+    }
+  }
+  return (double)(last - first) * 1000.0 / wall_khz_ / (double)count;
 }
 
 // Per-launch device timing over a preloaded trace: one step per launch (FUSED: one
@@ -1711,6 +1779,14 @@ int st_runtime_device_trace(st_runtime* r, const float* inputs, size_t count, do
   return guarded([&] {
     if (!r || !us_per_event) throw stamd::Error(ST_ERR_INVALID, "Null argument");
     *us_per_event = r->impl->device_trace(inputs, count, per_event_us);
+  });
+}
+
+int st_runtime_device_trace_noalloc(st_runtime* r, const float* device_events, size_t count, double* us_per_event,
+                                    double* per_event_us) {
+  return guarded([&] {
+    if (!r || !us_per_event) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    *us_per_event = r->impl->device_trace_noalloc(device_events, count, per_event_us);
   });
 }
 

@@ -400,9 +400,22 @@ __device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p, int buf, bool r
           poll_vector(c, a.t_in, a.features, a.features_p, c.epoch(0), xs);
           return;
         }
-        __amdgpu_buffer_rsrc_t ir = make_rsrc(c.input, (uint32_t)a.features_p * 4u);
-        for (int i = c.lane * 4; i < a.features_p; i += 256)
-          lds_store4(xs + i, ld16_coherent(ir, (uint32_t)i * 4u));
+        // The event holds `features` floats (any padding after them is not read): whole
+        // 16-byte pieces load at once, a partial last piece element by element, and the
+        // padded tail of the row is zero.
+        __amdgpu_buffer_rsrc_t ir = make_rsrc(c.input, (uint32_t)a.features * 4u);
+        for (int i = c.lane * 4; i < a.features_p; i += 256) {
+          float4 v;
+          if (i + 4 <= a.features) {
+            v = ld16_coherent(ir, (uint32_t)i * 4u);
+          } else {
+            float e[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) e[k] = i + k < a.features ? ld4_coherent(ir, (uint32_t)(i + k) * 4u) : 0.f;
+            v = make_float4(e[0], e[1], e[2], e[3]);
+          }
+          lds_store4(xs + i, v);
+        }
         return;
       }
       case kQkv:
@@ -1358,12 +1371,12 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(const StepArgs* __restr
 }
 
 // Device-only loop over a preloaded trace (the reference's trace_kernel): `count` steps in
-// one cooperative launch, with a wall-clock stamp per step from workgroup 0. Workgroup 0
-// publishes a step-done word after each FINAL; every workgroup waits for it before the
-// next step writes x.
+// one cooperative launch (event e at events + e * stride floats), with a wall-clock stamp per
+// step from workgroup 0. Workgroup 0 publishes a step-done word after each FINAL; every
+// workgroup waits for it before the next step writes x.
 template <int P, int A>
 __global__ __launch_bounds__(kThreads) void trace_kernel(const StepArgs* __restrict__ ap, const float* events, int count,
-                                                         unsigned long long* stamps) {
+                                                         int stride, unsigned long long* stamps) {
   const StepArgs& a = *ap;
   __shared__ LdsAll lds;
   Ctx<P> c(a, lds, (int)blockIdx.x, (int)gridDim.x);
@@ -1374,7 +1387,7 @@ __global__ __launch_bounds__(kThreads) void trace_kernel(const StepArgs* __restr
     if (blockIdx.x == 0 && threadIdx.x == 0) stamps[e] = wall_clock64();
     c.base = base0 + (unsigned)e * per_step;
     c.set_position(t0 + (unsigned long long)e);
-    c.input = events + (size_t)e * a.features_p;
+    c.input = events + (size_t)e * (size_t)stride;
     if (e > 0 && c.wave == 0) {
       float done[2];
       poll_pieces<P, 1>(c, a.t_done, 1, 0, 1, c.base - 1u, done);

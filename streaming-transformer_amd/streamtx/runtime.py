@@ -99,6 +99,7 @@ def library(path: os.PathLike | None = None) -> ctypes.CDLL:
     lib.st_runtime_snapshot.argtypes = [P, ctypes.POINTER(ctypes.c_uint64), F, F, F]
     lib.st_runtime_device_trace.argtypes = [P, F, ctypes.c_size_t, D, D]
     lib.st_runtime_device_run.argtypes = [P, F, ctypes.c_size_t, ctypes.c_int32, D, D]
+    lib.st_runtime_device_trace_noalloc.argtypes = [P, ctypes.c_void_p, ctypes.c_size_t, D, D]
     lib.st_runtime_phase_times.argtypes = [P, F, D, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     lib.st_runtime_trace_step.argtypes = [P, F, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t), F,
                                           ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
@@ -120,7 +121,8 @@ def library(path: os.PathLike | None = None) -> ctypes.CDLL:
     lib.st_batch_device_run.argtypes = [P, F, ctypes.c_size_t, D, D]
     for name in ('st_batch_create', 'st_batch_step', 'st_batch_reset', 'st_batch_snapshot', 'st_batch_device_run',
                  'st_runtime_create', 'st_runtime_step', 'st_runtime_reset', 'st_runtime_stop',
-                 'st_runtime_snapshot', 'st_runtime_device_trace', 'st_runtime_device_run', 'st_runtime_phase_times',
+                 'st_runtime_snapshot', 'st_runtime_device_trace', 'st_runtime_device_trace_noalloc',
+                 'st_runtime_device_run', 'st_runtime_phase_times',
                  'st_runtime_trace_step', 'st_runtime_scheduled_run',
                  'st_runtime_info_json',
                  'st_probe_json', 'st_transport_bench'):
@@ -262,6 +264,17 @@ class Runtime:
         mean = ctypes.c_double(0)
         _check(library().st_runtime_device_trace(self._handle(), _fptr(x), x.shape[0], ctypes.byref(mean),
                                                  per.ctypes.data_as(ctypes.POINTER(ctypes.c_double))))
+        return float(mean.value), per
+
+    def device_trace_noalloc(self, device_events: int, count: int, per_event: bool = True):
+        """st_runtime_device_trace_noalloc: `count` events already in device memory at address
+        `device_events` (count*features floats, unpadded); the call allocates nothing.
+        (mean us, per-event us or None)."""
+        per = np.empty(count, dtype=np.float64) if per_event else None
+        mean = ctypes.c_double(0)
+        _check(library().st_runtime_device_trace_noalloc(
+            self._handle(), ctypes.c_void_p(device_events), int(count), ctypes.byref(mean),
+            per.ctypes.data_as(ctypes.POINTER(ctypes.c_double)) if per is not None else None))
         return float(mean.value), per
 
     def device_run(self, inputs, reset: bool = False):
