@@ -661,43 +661,46 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* 
   float acc0 = 0.f, acc1 = 0.f;
   // Lane k holds the row sums of the k-th unit finished since the last epilogue batch. The
   // epilogues (whose tagged stores are written through to memory) run after the ring loop:
-  // the loop's back edge and exit wait for every outstanding vector memory operation of
-  // the wave (vmcnt(0)), and stores issued inside the loop would make the wave wait for
-  // their write acknowledgements before it signals completion and prefetches the next phase.
+  // stores issued inside it would count against the same vmcnt as the ring's loads, and the
+  // ring's waits would then also wait for their write acknowledgements.
   float su0 = 0.f, su1 = 0.f;
   int finished = 0;
   const float* xs = xs_buf + c.lane * Traits<P>::kEpc;
+  // One slab: its dot product into the current row's sum, then the row / unit bookkeeping.
+  auto consume = [&](const uint4& slab) {
+    const float d = chunk_dot<P>(slab, xs + s * 64 * Traits<P>::kEpc);
+    if (ru == 0) acc0 += d; else acc1 += d;
+    if (++s == w.slabs_row) {
+      s = 0;
+      if (++ru == munit) {
+        ru = 0;
+        const float s0 = wave_total(acc0);
+        const float s1 = munit == 2 ? wave_total(acc1) : 0.f;
+        if (c.lane == finished) {
+          su0 = s0;
+          su1 = s1;
+        }
+        finished++;
+        acc0 = 0.f;
+        acc1 = 0.f;
+      }
+    }
+  };
   if (c.wave == 1) stamp(c, p, 4);
-  for (int base = 0; base < w.slabs; base += kPF) {
+  // Every pass but the last consumes all kPF ring slots and refills each one right after
+  // consuming it, unconditionally (past the wave's last slab it reloads that slab, which is
+  // cached): every pass then issues exactly kPF loads in ring order, so before slot j the
+  // wave waits only for slot j's own load and keeps kPF - 1 loads in flight. With refills
+  // under a condition, the compiler could not count the outstanding loads across the back
+  // edge and waited for all of them at the start of every pass.
+  const int full = (w.slabs - 1) / kPF;
+  for (int pass = 0; pass < full; pass++) {
 #pragma unroll
     for (int j = 0; j < kPF; j++) {
-      if (base + j < w.slabs) {
-        float d = chunk_dot<P>(ring[j], xs + s * 64 * Traits<P>::kEpc);
-        if (j == 0 && base == 0 && c.a.stamps && c.wave == 1) {
-          asm volatile("" ::"v"(d));
-          stamp(c, p, 5);
-        }
-        if (ru == 0) acc0 += d; else acc1 += d;
-        if (base + j + kPF < w.slabs) {
-          ring[j] = ld16(c.wr, refill.offset(c.lane));
-          refill.advance(w);
-        }
-        if (++s == w.slabs_row) {
-          s = 0;
-          if (++ru == munit) {
-            ru = 0;
-            float s0 = wave_total(acc0);
-            float s1 = munit == 2 ? wave_total(acc1) : 0.f;
-            if (c.lane == finished) {
-              su0 = s0;
-              su1 = s1;
-            }
-            finished++;
-            acc0 = 0.f;
-            acc1 = 0.f;
-          }
-        }
-      }
+      consume(ring[j]);
+      const bool more = pass * kPF + j + kPF < w.slabs;
+      ring[j] = ld16(c.wr, (more ? refill : last).offset(c.lane));
+      if (more) refill.advance(w);
     }
     // At most kPF units finish in one pass (a unit has at least one slab): flush the batch
     // inside the loop only when the next pass could overflow the 64 lanes (very small grids).
@@ -707,6 +710,10 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* 
       finished = 0;
     }
   }
+  // The last pass: the remaining 1..kPF slabs, no refills.
+#pragma unroll
+  for (int j = 0; j < kPF; j++)
+    if (full * kPF + j < w.slabs) consume(ring[j]);
   // Epilogues of the finished units, one unit per lane.
   if (c.lane < finished) epilogue(c, p, unit + kStreamWaves * c.lane, su0, su1, xres);
   if (c.wave == 1) stamp(c, p, 6);
@@ -1321,7 +1328,11 @@ __device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
     {
       // With the attention K/V in LDS the ring has nothing to prefetch for attention. It
       // stays empty, so that the attention phase's stores and polls find this CU's memory
-      // queue empty; OUT is prefetched after attention.
+      // queue empty; OUT is prefetched after attention. QKV's weights are not prefetched
+      // either, but loaded when its phase starts: every CU's bulk loads slow the polls of
+      // the DOWN -> QKV exchange, which costs more than the prefetch saves (Large 350 ->
+      // 339 us, Main 156 -> 152 us). Issuing them as soon as this CU's own poll of x has
+      // returned was slower again (351 us): other CUs are still polling then.
       const Phase nxt = phase_of(a, ph + 1);
       if (!(A == 1 && c.kv_lds && nxt.kind == kAttn)) prefetch(c, nxt, ring);
     }
