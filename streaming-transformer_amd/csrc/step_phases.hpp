@@ -1328,11 +1328,8 @@ __device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
     {
       // With the attention K/V in LDS the ring has nothing to prefetch for attention. It
       // stays empty, so that the attention phase's stores and polls find this CU's memory
-      // queue empty; OUT is prefetched after attention. QKV's weights are not prefetched
-      // either, but loaded when its phase starts: every CU's bulk loads slow the polls of
-      // the DOWN -> QKV exchange, which costs more than the prefetch saves (Large 350 ->
-      // 339 us, Main 156 -> 152 us). Issuing them as soon as this CU's own poll of x has
-      // returned was slower again (351 us): other CUs are still polling then.
+      // queue empty; OUT is prefetched after attention. (Waves without OUT rows prefetching
+      // their GATEUP share here instead was slower: Large 323 -> 329 us, Main 152 -> 161 us.)
       const Phase nxt = phase_of(a, ph + 1);
       if (!(A == 1 && c.kv_lds && nxt.kind == kAttn)) prefetch(c, nxt, ring);
     }

@@ -28,6 +28,33 @@ def hipcc() -> str:
     raise RuntimeError('hipcc not found')
 
 
+HARNESS_DIR = PACKAGE_DIR / 'harness'
+HARNESS = OUTPUT.parent / 'stream-bench'
+TESTS_DIR = PACKAGE_DIR.parent / 'tests'
+ABI_CONSUMER = TESTS_DIR / '_build' / 'abi_consumer'
+HARNESS_SELFTEST = TESTS_DIR / '_build' / 'harness_selftest'
+
+
+def _cxx(source: Path, output: Path, rpath: str) -> None:
+    """A host-only C++ consumer of the C ABI, linked against libstamd.so."""
+    output.parent.mkdir(parents=True, exist_ok=True)
+    cmd = [os.environ.get('CXX', 'g++'), '-O2', '-std=c++17', '-Wall', '-Wextra',
+           f'-I{PACKAGE_DIR.parent / "include"}', f'-I{HARNESS_DIR}', '-o', str(output), str(source),
+           f'-L{OUTPUT.parent}', '-lstamd', f'-Wl,-rpath,{rpath}', '-pthread']
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f'{cmd[0]} failed ({proc.returncode}):\n{proc.stderr[-4000:]}')
+
+
+def build_consumers() -> tuple[Path, Path, Path]:
+    """The benchmark driver (stream-bench, next to the library), and two test programs under
+    tests/_build (test infrastructure): the C++ ABI consumer and the driver's self-test."""
+    _cxx(HARNESS_DIR / 'stream_bench.cpp', HARNESS, '$ORIGIN')
+    _cxx(TESTS_DIR / 'abi_consumer.cpp', ABI_CONSUMER, '$ORIGIN/../../streaming-transformer_amd/lib')
+    _cxx(TESTS_DIR / 'harness_selftest.cpp', HARNESS_SELFTEST, '$ORIGIN/../../streaming-transformer_amd/lib')
+    return HARNESS, ABI_CONSUMER, HARNESS_SELFTEST
+
+
 def build(force: bool = True, verbose: bool = False) -> Path:
     """Compile libstamd.so. With force=False, skip when the library is newer than its sources."""
     if not force and OUTPUT.exists():

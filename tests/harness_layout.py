@@ -1,0 +1,78 @@
+"""Reference-layout fixture directories for the benchmark driver's tests.
+
+The driver (stream-bench) reads fixtures the way the reference's bench/Main.cpp does:
+`--weights DIR` holding manifest.json + tensors.bin (the checkpoint), trace.bin and
+resets.json, with the expected outputs in DIR/expected/ (manifest.json + tensors.bin holding
+float32 scores[E], hidden[E,L,d], keys/values[E,L,H,W,dh]; reference/export.py:46-70), and a
+config file equal to the checkpoint's config. tests/golden keeps the reference's small
+fixtures compactly (the K/V row written by each event instead of the full cache per event);
+this helper expands them back into that layout.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import shutil
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE / 'golden'))
+from make_golden import rebuild_cache  # noqa: E402
+
+GOLDEN = HERE / 'golden'
+
+
+def write_archive(directory: Path, tensors: dict, **fields) -> None:
+    """manifest.json + tensors.bin with float32 tensors, the archive SHA-256 and extra fields."""
+    directory.mkdir(parents=True, exist_ok=True)
+    data = bytearray()
+    table = []
+    for name, array in tensors.items():
+        blob = np.ascontiguousarray(array, dtype='<f4').tobytes()
+        table.append(dict(name=name, shape=list(np.shape(array)), dtype='float32', offset=len(data), nbytes=len(blob),
+                          sha256=hashlib.sha256(blob).hexdigest()))
+        data.extend(blob)
+    (directory / 'tensors.bin').write_bytes(bytes(data))
+    manifest = dict(fields, tensors=table, sha256=hashlib.sha256(bytes(data)).hexdigest())
+    (directory / 'manifest.json').write_text(json.dumps(manifest, indent=2) + '\n')
+
+
+def reference_fixture(name: str, target: Path) -> tuple[Path, Path]:
+    """Expand tests/golden/<name> into target/ in the reference's layout.
+    Returns (weights directory, config file)."""
+    source = GOLDEN / name
+    target.mkdir(parents=True, exist_ok=True)
+    for f in ('manifest.json', 'tensors.bin'):
+        shutil.copyfile(source / 'checkpoint' / f, target / f)
+    for f in ('trace.bin', 'resets.json'):
+        shutil.copyfile(source / f, target / f)
+    manifest = json.loads((source / 'checkpoint' / 'manifest.json').read_text())
+    config = manifest['config']
+    expected = np.load(source / 'expected.npz')
+    resets = set(int(r) for r in expected['resets'])
+    keys = np.stack([c.copy() for c in rebuild_cache(expected['key_rows'], resets, config['window'])])
+    values = np.stack([c.copy() for c in rebuild_cache(expected['value_rows'], resets, config['window'])])
+    write_archive(target / 'expected', dict(scores=expected['scores'], hidden=expected['hidden'], keys=keys,
+                                            values=values),
+                  version=1, byte_order='little', orientation='out_in', config=config, mode=manifest['mode'],
+                  resets=sorted(resets))
+    config_file = target / 'config.json'
+    config_file.write_text(json.dumps(config, indent=2) + '\n')
+    return target, config_file
+
+
+def reference_checkpoint(name: str, target: Path) -> tuple[Path, Path]:
+    """tests/golden/<name> (a checkpoint and its trace, no expected outputs) in the reference's
+    layout. Returns (weights directory, config file)."""
+    source = GOLDEN / name
+    target.mkdir(parents=True, exist_ok=True)
+    for f in ('manifest.json', 'tensors.bin'):
+        shutil.copyfile(source / 'checkpoint' / f, target / f)
+    shutil.copyfile(source / 'trace.bin', target / 'trace.bin')
+    config = json.loads((source / 'checkpoint' / 'manifest.json').read_text())['config']
+    config_file = target / 'config.json'
+    config_file.write_text(json.dumps(config, indent=2) + '\n')
+    return target, config_file

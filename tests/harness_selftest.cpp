@@ -1,0 +1,91 @@
+// Checks of the benchmark driver's building blocks that need no GPU (test infrastructure):
+//  - SHA-256 known answers (FIPS 180-4 examples; the reference's tests/Native.cpp:18-22 pins
+//    sha256("abc")), including inputs that cross the 64-byte block and padding boundaries;
+//  - nearest-rank percentiles (the reference's tests/test_analysis.py:9-12);
+//  - the Errors thresholds at their edges, FP32 and mixed (bench/Main.cpp:57-84);
+//  - JSON round trips and equality as the driver uses them.
+// With the argument "halves" it prints the FP32 bits of every FP16 bit pattern's decode, one
+// hex word per line, for the Python test to compare with numpy.
+#include "json.hpp"
+#include "metrics.hpp"
+#include "model.hpp"
+#include "sha256.hpp"
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using namespace stbench;
+
+static int failures = 0;
+static void expect(bool ok, const char* what) {
+  if (!ok) {
+    failures++;
+    std::printf("FAIL %s\n", what);
+  }
+}
+
+int main(int argc, char** argv) {
+  if (argc > 1 && std::string(argv[1]) == "halves") {
+    for (unsigned h = 0; h < 65536; h++) {
+      const float f = half_to_float((uint16_t)h);
+      uint32_t bits;
+      std::memcpy(&bits, &f, 4);
+      std::printf("%08x\n", bits);
+    }
+    return 0;
+  }
+  expect(sha256("abc", 3) == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad", "sha256(abc)");
+  expect(sha256("", 0) == "e3b0c44298fc1c149afbf4c8996fb92427ae41e4649b934ca495991b7852b855", "sha256(empty)");
+  const char* two = "abcdbcdecdefdefgefghfghighijhijkijkljklmklmnlmnomnopnopq";
+  expect(sha256(two, std::strlen(two)) == "248d6a61d20638b8e5c026930c3e6039a33ce45964ff2167f6ecedd419db06c1",
+         "sha256(448-bit message)");
+  std::vector<char> million(1000000, 'a');
+  Sha256 incremental;
+  for (size_t i = 0; i < million.size(); i += 997) incremental.update(million.data() + i, std::min<size_t>(997, million.size() - i));
+  expect(incremental.hex() == "cdc76e5c9914fb9281a1c7e284d73e67f1809a48a497200e046d39ccc7112cd0",
+         "sha256(one million 'a', fed in 997-byte pieces)");
+
+  std::vector<double> v;
+  for (int i = 1; i <= 100; i++) v.push_back(i);
+  Json d = distribution(v);
+  expect(d.at("p50_us").number() == 50 && d.at("p95_us").number() == 95 && d.at("p99_us").number() == 99 &&
+             d.at("p999_us_diagnostic").number() == 100 && d.at("worst_us").number() == 100,
+         "nearest-rank percentiles of 1..100");
+  expect(distribution({7.0}).at("p50_us").number() == 7 && distribution({}).size() == 0, "one sample / no samples");
+
+  Errors e;
+  e.check(1.0f, 1.0f, false);
+  e.check(1.0f + 1.05e-4f, 1.0f, false);  // within 1e-5 + 1e-4
+  e.check(1.0f + 1.2e-4f, 1.0f, false);   // beyond
+  e.check(NAN, 1.0f, false);
+  expect(e.count == 4 && e.failed == 2 && e.nonfinite == 1, "FP32 thresholds and non-finite values");
+  Errors m;
+  m.check(0.0f, 0.0f, true, 3);
+  m.check(5.9e-3f, 0.0f, true, 3);   // within 2e-3 * 3
+  m.check(6.1e-3f, 0.0f, true, 3);   // beyond
+  m.check(10.2f, 10.0f, true, 1);    // within 2e-3 + 2e-2 * 10
+  m.check(10.3f, 10.0f, true, 1);    // beyond
+  expect(m.count == 5 && m.failed == 2, "mixed thresholds with the absolute scale");
+  const float ref[4] = {3, 4, 0, 0}, act[4] = {3, 4, 0, 1};
+  expect(std::fabs(relative_l2(act, ref, 4) - 0.2) < 1e-12 && residual_scale(ref, 4) == 2.5 &&
+             mixed_state_scale(ref, 4, 2) == 7.5,
+         "relative L2, residual scale and the mixed state scale");
+
+  const Json j = Json::parse(R"({"b": [1, 2.5, -3, true, null, "x\"yé"], "a": {"n": 18446744073709551615}})");
+  expect(j.at("a").at("n").uinteger() == 18446744073709551615ull, "64-bit unsigned integers");
+  expect(Json::parse(j.dump(2)) == j && Json::parse(j.dump()) == j, "dump / parse round trip");
+  expect(Json::parse(R"({"x": 1, "y": 1e-05})") == Json::parse(R"({"y": 0.00001, "x": 1})"), "object equality");
+  expect(Json::parse("[1]") != Json::parse("[1.5]"), "number inequality");
+  bool threw = false;
+  try {
+    Json::parse("{\"a\": 1,}");
+  } catch (const std::runtime_error&) {
+    threw = true;
+  }
+  expect(threw, "malformed JSON rejected");
+
+  std::printf("%s: %d failure(s)\n", failures ? "FAILED" : "OK", failures);
+  return failures ? 1 : 0;
+}
