@@ -83,7 +83,8 @@ def batched_streams(counts=(1, 16, 64, 256), steps=64, mode='bf16w'):
         gbs = step_bytes / (mean * 1e-6) / 1e9
         out[f'B{b}'] = {'p50_us_per_step': round(p50, 2), 'mean_us_per_step': round(mean, 2),
                         'events_per_s': round(b / (p50 * 1e-6)), 'algorithmic_bytes_per_step': step_bytes,
-                        'achieved_gbs': round(gbs, 1), 'hbm_frac': round(gbs / HBM_PEAK_GBS, 4)}
+                        'achieved_gbs': round(gbs, 1), 'hbm_frac': round(gbs / HBM_PEAK_GBS, 4),
+                        'mall_resident': step_bytes < 256e6}
     return out
 
 
@@ -214,9 +215,86 @@ def window_sweep(windows=(32, 64, 128, 256, 512), steps=2048):
             step_bytes = weight_bytes_per_step(c, 2) + kv_bytes_per_step(c, 2 if mixed else 4, w)
             gbs = step_bytes / (mean * 1e-6) / 1e9
             rows[f'W{w}'] = {'p50_us': round(nearest_rank(per, 0.5), 2), 'p99_us': round(nearest_rank(per, 0.99), 2),
-                             'algorithmic_bytes_per_step': step_bytes, 'achieved_gbs': round(gbs, 1)}
+                             'algorithmic_bytes_per_step': step_bytes, 'achieved_gbs': round(gbs, 1),
+                             'mall_resident': step_bytes < 256e6}
         out[mode] = rows
     return out
+
+
+def main_backends(steps=512):
+    """Main FP32 (d 512, 8 layers, W 128; 140 MB per step, resident in the 256 MB Infinity
+    Cache), one stream, seed 1, through the fused, graph and staged backends (device p50 per
+    step, HIP events between launches) and the persistent worker (host service through step(),
+    PCIe-inclusive)."""
+    c, seed = CONFIGS['main']
+    weights = synthetic_checkpoint(c, seed=seed)
+    events = np.random.default_rng([seed, 1]).standard_normal((c.window - 1 + 64 + steps, c.features),
+                                                               dtype=np.float32)
+    fill = c.window - 1 + 64
+    step_bytes = weight_bytes_per_step(c, 4) + kv_bytes_per_step(c, 4, c.window)
+    out = {'workload': 'main fp32 single-stream step, W=128', 'steps': steps, 'algorithmic_bytes_per_step': step_bytes,
+           'mall_resident': step_bytes < 256e6}
+    for name, backend in (('fused', Backend.FUSED), ('graph', Backend.GRAPH), ('staged', Backend.CUDA)):
+        with Runtime((c, weights, False), RuntimeOptions(backend=backend, blocks=0)) as rt:
+            rt.device_run(events[:fill], reset=True)
+            mean, per = rt.device_run(events[fill:fill + steps])
+        out[name] = {'p50_us': round(nearest_rank(per, 0.5), 2), 'p99_us': round(nearest_rank(per, 0.99), 2),
+                     'roofline_frac': round(step_bytes / (mean * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    with Runtime((c, weights, False), RuntimeOptions(backend=Backend.PERSISTENT, blocks=0)) as rt:
+        for e in events[:fill]:
+            rt.step(e)
+        host = []
+        for e in events[fill:fill + steps]:
+            s = time.perf_counter()
+            rt.step(e)
+            host.append((time.perf_counter() - s) * 1e6)
+    out['persistent_service'] = {'p50_us': round(nearest_rank(host, 0.5), 2), 'p99_us': round(nearest_rank(host, 0.99), 2)}
+    return out
+
+
+def matvec_bandwidth(rt, c: ModelConfig, events, wb: int, kvb: int):
+    """Achieved GB/s of each matvec kind inside the fused step, from the per-phase wall-clock
+    stamps of st_runtime_phase_times over len(events) full-window steps. Bytes of a phase:
+    its weight rows (QKV 3d x d, OUT d x d, GATEUP 2F x d, DOWN d x F; norm weights and padding
+    excluded); ATTN: the K/V rows of the window. `phase_us` runs from one phase's start to the
+    next one's (median over workgroups, layers and steps): it includes the exchange of the next
+    phase's input. `compute_us` ends when this workgroup's stream waves are done with the phase.
+    Recording the stamps adds a few LDS stores per phase and workgroup."""
+    d, F, L = c.width, c.ffn, c.layers
+    weights = {'QKV': 3 * d * d * wb, 'OUT': d * d * wb, 'GATEUP': 2 * F * d * wb, 'DOWN': d * F * wb,
+               'ATTN': 2 * d * c.window * kvb}
+    kinds = ['INPUT'] + [k for _ in range(L) for k in ('QKV', 'ATTN', 'OUT', 'GATEUP', 'DOWN')] + ['FINAL']
+    phase, compute = {k: [] for k in weights}, {k: [] for k in weights}
+    for e in events:
+        st, _ = rt.phase_times(e)
+        for ph, kind in enumerate(kinds[:-1]):
+            if kind not in weights:
+                continue
+            s0 = st[ph, :, 0]
+            phase[kind].append(float(np.median(st[ph + 1, :, 0] - s0)))
+            compute[kind].append(float(np.median(st[ph, :, 2] - s0)))
+    out = {}
+    for kind, b in weights.items():
+        pu, cu = float(np.median(phase[kind])), float(np.median(compute[kind]))
+        out[kind] = {'bytes_per_layer': b, 'phase_us': round(pu, 2), 'compute_us': round(cu, 2),
+                     'gbs_phase': round(b / (pu * 1e-6) / 1e9, 1), 'gbs_compute': round(b / (cu * 1e-6) / 1e9, 1)}
+    return out
+
+
+def host_cpu():
+    """CPU model and hardware thread count of this host (from /proc/cpuinfo)."""
+    model, threads, flags = 'unknown', 0, set()
+    try:
+        for line in Path('/proc/cpuinfo').read_text().splitlines():
+            if line.startswith('model name') and model == 'unknown':
+                model = line.split(':', 1)[1].strip()
+            elif line.startswith('processor'):
+                threads += 1
+            elif line.startswith('flags') and not flags:
+                flags = set(line.split(':', 1)[1].split())
+    except OSError:
+        pass
+    return model, threads, flags
 
 
 def nearest_rank(values, q):
@@ -224,19 +302,19 @@ def nearest_rank(values, q):
     return float(v[max(0, int(math.ceil(q * len(v))) - 1)])
 
 
-def cpu_baseline(c: ModelConfig, weights, mixed, events, fill: int, sample: int):
+def cpu_baseline(c: ModelConfig, weights, mixed, events, fill: int, sample: int, isa: str):
     """The C oracle (a restatement of the reference CPU step) timed on this host:
-    single thread (the reference default), on `sample` full-window steps."""
+    single thread (the reference default), on `sample` full-window steps, then with an
+    OpenMP split over matvec rows on up to 16 threads. isa: 'v3' (the AVX2 build) or
+    'portable'."""
     from oracle.pyoracle import Oracle
     threads_all = min(16, os.cpu_count() or 1)
-    oracle = Oracle(c, weights, mixed=mixed, threads=threads_all)
+    oracle = Oracle(c, weights, mixed=mixed, threads=threads_all, isa=isa)
     for e in events[:fill]:
         oracle.step(e)
     out = {}
     for threads in (1, threads_all):
-        oracle_threads = threads
-        from oracle import pyoracle
-        pyoracle.library().so_set_threads(oracle._h, oracle_threads)
+        oracle._lib.so_set_threads(oracle._h, threads)
         times = []
         for e in events[fill:fill + sample]:
             t0 = time.perf_counter()
@@ -352,6 +430,9 @@ def main():
                 n = c.window - 1 + 256
                 _, loop = rt.device_trace(events[:n])
                 extra['device_loop_p50_us'] = nearest_rank(loop[c.window - 1:], 0.5)
+                # Achieved GB/s of each matvec kind within the step (phase stamps).
+                rt.device_run(events[:fill], reset=True)
+                extra['matvec_gbs'] = matvec_bandwidth(rt, c, events[fill:fill + 8], wb, kvb)
     if not args.quick and backend == Backend.FUSED:
         # Same service latency through the persistent mailbox worker (no launch per step).
         popts = RuntimeOptions(backend=Backend.PERSISTENT, blocks=0, weight_dtype=opts.weight_dtype)
@@ -419,6 +500,8 @@ def main():
         extra['batched'] = batched_streams()
         extra['batched_mixed'] = batched_streams(mode='mixed')
         extra['window_sweep'] = window_sweep()
+        if args.config == 'large' and args.precision == 'fp32' and backend == Backend.FUSED:
+            extra['main_fp32'] = main_backends()
 
     achieved = bytes_step / (mean_us * 1e-6) / 1e9
     roofline = {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
@@ -436,15 +519,19 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        sample = {'large': 12, 'main': 40, 'small': 200}[args.config]
-        cfill = {'large': c.window - 1, 'main': c.window - 1, 'small': c.window - 1}[args.config]
+        sample = {'large': 24, 'main': 80, 'small': 400}[args.config]
+        cfill = c.window - 1
+        model, host_threads, flags = host_cpu()
+        isa = 'v3' if {'avx2', 'fma', 'bmi2'} <= flags else 'portable'
         times, threads_all = cpu_baseline(c, weights if args.precision != 'bf16w' else
                                           {k: __import__('streamtx').round_bf16(v) for k, v in weights.items()},
-                                          mixed, events, cfill, sample)
+                                          mixed, events, cfill, sample, isa)
         cpu = {'value': nearest_rank(times[1], 0.5), 'unit': 'us per step (p50)', 'cores': 1,
                'kind': 'port',
                'sample': f'{sample} full-window steps of the same {args.config} {args.precision} workload after a '
-                         f'{cfill}-event fill; C oracle restating src/cpu/Cpu.cpp:59-141, 1 thread',
+                         f'{cfill}-event fill; C oracle restating src/cpu/Cpu.cpp:59-141, 1 thread, built '
+                         f'-O3 {"-march=x86-64-v3 " if isa == "v3" else ""}-ffp-contract=off',
+               'cpu_model': model, 'host_threads': host_threads, 'isa': isa,
                'multithread_p50_us': nearest_rank(times[threads_all], 0.5), 'multithread_cores': threads_all}
 
     line = {

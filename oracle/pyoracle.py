@@ -14,6 +14,8 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 LIBRARY = HERE / '_build' / 'libstream_oracle.so'
+# The same C source built for x86-64-v3 (AVX2) hosts, for timing; bit-identical results.
+LIBRARY_V3 = HERE / '_build' / 'libstream_oracle_v3.so'
 
 # Canonical tensor order of so_create (oracle/stream_oracle.h).
 _LAYER_ORDER = ('norm1', 'norm2', 'q', 'k', 'v', 'out', 'gate', 'up', 'down')
@@ -25,7 +27,7 @@ class _Config(ctypes.Structure):
                 ('epsilon', ctypes.c_float)]
 
 
-_lib = None
+_libs = {}
 
 
 def build() -> Path:
@@ -33,12 +35,13 @@ def build() -> Path:
     return LIBRARY
 
 
-def library() -> ctypes.CDLL:
-    global _lib
-    if _lib is None:
-        if not LIBRARY.exists():
+def library(isa: str = 'portable') -> ctypes.CDLL:
+    """The oracle library: 'portable' (x86-64 baseline) or 'v3' (AVX2 hosts)."""
+    if isa not in _libs:
+        path = LIBRARY if isa == 'portable' else LIBRARY_V3
+        if not path.exists():
             build()
-        lib = ctypes.CDLL(str(LIBRARY))
+        lib = ctypes.CDLL(str(path))
         F = ctypes.POINTER(ctypes.c_float)
         lib.so_create.argtypes = [ctypes.POINTER(_Config), ctypes.c_int, ctypes.c_int, ctypes.POINTER(F)]
         lib.so_create.restype = ctypes.c_void_p
@@ -58,8 +61,8 @@ def library() -> ctypes.CDLL:
         lib.so_half_bits.restype = ctypes.c_uint16
         lib.so_bf16_bits.argtypes = [ctypes.c_float]
         lib.so_bf16_bits.restype = ctypes.c_uint16
-        _lib = lib
-    return _lib
+        _libs[isa] = lib
+    return _libs[isa]
 
 
 def _fptr(a):
@@ -71,10 +74,12 @@ class Oracle:
 
     config: any object with layers/width/heads/ffn/window/features/epsilon; tensors: name ->
     float32 array. accumulate: 'float' (the reference's arithmetic) or 'double' (referee).
+    isa: 'portable' or 'v3' (the AVX2 build, same results; used to time the CPU baseline).
     """
 
-    def __init__(self, config, tensors, mixed=False, accumulate='float', threads=1):
+    def __init__(self, config, tensors, mixed=False, accumulate='float', threads=1, isa='portable'):
         self.config = config
+        self._lib = library(isa)
         self.mixed = bool(mixed)
         names = ['input', 'final_norm', 'score']
         for layer in range(config.layers):
@@ -83,27 +88,27 @@ class Oracle:
         ptrs = (ctypes.POINTER(ctypes.c_float) * len(names))(*[_fptr(a) for a in self._keep])
         cfg = _Config(config.layers, config.width, config.heads, config.ffn, config.window, config.features,
                       config.epsilon)
-        self._h = library().so_create(ctypes.byref(cfg), int(self.mixed), int(accumulate == 'double'), ptrs)
+        self._h = self._lib.so_create(ctypes.byref(cfg), int(self.mixed), int(accumulate == 'double'), ptrs)
         if not self._h:
             raise ValueError('Invalid or unsupported model dimensions')
         if threads > 1:
-            library().so_set_threads(self._h, threads)
+            self._lib.so_set_threads(self._h, threads)
 
     def __del__(self):
         if getattr(self, '_h', None):
-            library().so_destroy(self._h)
+            self._lib.so_destroy(self._h)
             self._h = None
 
     def step(self, event) -> float:
         x = np.ascontiguousarray(event, dtype=np.float32)
-        return float(library().so_step(self._h, _fptr(x)))
+        return float(self._lib.so_step(self._h, _fptr(x)))
 
     def reset(self) -> None:
-        library().so_reset(self._h)
+        self._lib.so_reset(self._h)
 
     @property
     def position(self) -> int:
-        return int(library().so_position(self._h))
+        return int(self._lib.so_position(self._h))
 
     def snapshot(self):
         c = self.config
@@ -111,7 +116,7 @@ class Oracle:
         keys = np.empty((c.layers, c.heads, c.window, dim), dtype=np.float32)
         values = np.empty_like(keys)
         hidden = np.empty((c.layers, c.width), dtype=np.float32)
-        library().so_snapshot(self._h, _fptr(keys), _fptr(values), _fptr(hidden))
+        self._lib.so_snapshot(self._h, _fptr(keys), _fptr(values), _fptr(hidden))
         return self.position, keys, values, hidden
 
 

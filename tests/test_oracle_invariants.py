@@ -234,3 +234,25 @@ def test_float_and_double_accumulation_agree_at_baseline_shapes(name, config, st
     _, kd, vd, hd = d.snapshot()
     for a, b in ((kf, kd), (vf, vd), (hf, hd)):
         assert numerical.fp32_strict_failures(a, b) == 0
+
+
+def test_avx2_build_is_bit_identical_to_portable_build():
+    """The x86-64-v3 oracle build that times the CPU baseline computes the same bits as the
+    portable build the tests use (no FMA contraction, no reassociation in either)."""
+    flags = set()
+    for line in open('/proc/cpuinfo').read().splitlines():
+        if line.startswith('flags'):
+            flags = set(line.split(':', 1)[1].split())
+            break
+    if not {'avx2', 'fma', 'bmi2'} <= flags:
+        pytest.skip('host without AVX2')
+    from oracle.pyoracle import Oracle
+    from streamtx import ModelConfig, synthetic_checkpoint
+    c = ModelConfig(2, 256, 4, 512, 16, 128)
+    for mixed in (False, True):
+        w = synthetic_checkpoint(c, seed=5, mixed=mixed)
+        ev = np.random.default_rng(5).standard_normal((40, c.features), dtype=np.float32)
+        a, b = Oracle(c, w, mixed=mixed), Oracle(c, w, mixed=mixed, isa='v3')
+        assert [a.step(e) for e in ev] == [b.step(e) for e in ev]
+        for x, y in zip(a.snapshot()[1:], b.snapshot()[1:]):
+            assert np.array_equal(x, y)
