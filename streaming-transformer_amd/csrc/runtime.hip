@@ -286,7 +286,9 @@ class Runtime {
   void sync() { HIP_CHECK(hipStreamSynchronize(stream_)); }
   bool persistent() const { return opt_.backend == ST_BACKEND_PERSISTENT; }
   bool coresident(int grid);
-  bool plain_launch_ = false;  // FUSED (and GRAPH's fused node): the grid passed the co-residency probe
+  // grid_ passed the co-residency probe: the FUSED, PERSISTENT and trace kernels (and GRAPH's
+  // fused node) launch plainly.
+  bool plain_launch_ = false;
   bool graph_fused_ = false;   // GRAPH: the captured step is the fused kernel
   bool vendor() const { return opt_.backend == ST_BACKEND_CUBLAS || opt_.backend == ST_BACKEND_CUBLAS_GRAPH; }
   void reset_device();
@@ -544,7 +546,12 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
       else launch_phases();
     });
   }
-  if (options.backend == ST_BACKEND_FUSED && grid_ > 1) plain_launch_ = coresident(grid_);
+  // FUSED, PERSISTENT and the device trace launch grid_ workgroups plainly when the probe
+  // shows them resident at once. A cooperative launch is the fallback only: it takes the
+  // device's global wave sync resource, which one process holds at a time, so while another
+  // process holds it a cooperative launch fails (hipErrorIllegalState).
+  if (!plain_launch_ && grid_ > 1 && options.backend != ST_BACKEND_GRAPH && !vendor())
+    plain_launch_ = coresident(grid_);
   if (persistent()) {
     if (epoch_ + 2ull * per_step() > kEpochLimit) rebase_epochs();
     start_worker();
@@ -872,9 +879,9 @@ void Runtime::stop() {
 }
 
 template <int P, int A>
-static void launch_persistent_t(int grid, const StepArgs* dargs, hipStream_t stream) {
-  if (grid == 1) {
-    hipLaunchKernelGGL((persistent_kernel<P, A>), dim3(1), dim3(kThreads), 0, stream, dargs);
+static void launch_persistent_t(int grid, bool plain, const StepArgs* dargs, hipStream_t stream) {
+  if (grid == 1 || plain) {
+    hipLaunchKernelGGL((persistent_kernel<P, A>), dim3(grid), dim3(kThreads), 0, stream, dargs);
   } else {
     void* params[] = {&dargs};
     HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<void*>(persistent_kernel<P, A>), dim3(grid), dim3(kThreads),
@@ -885,7 +892,7 @@ static void launch_persistent_t(int grid, const StepArgs* dargs, hipStream_t str
 
 void Runtime::start_worker() {
   dispatch([&](auto P, auto A) {
-    launch_persistent_t<P.value, A.value>(grid_, dargs_, stream_);
+    launch_persistent_t<P.value, A.value>(grid_, plain_launch_, dargs_, stream_);
     return 0;
   });
 }
@@ -998,8 +1005,9 @@ void Runtime::snapshot(uint64_t* position, float* keys, float* values, float* hi
 
 template <int P, int A>
 void Runtime::launch_trace_t(const float* events, int count, int stride, unsigned long long* stamps) {
-  if (grid_ == 1) {
-    hipLaunchKernelGGL((trace_kernel<P, A>), dim3(1), dim3(kThreads), 0, stream_, dargs_, events, count, stride, stamps);
+  if (grid_ == 1 || plain_launch_) {
+    hipLaunchKernelGGL((trace_kernel<P, A>), dim3(grid_), dim3(kThreads), 0, stream_, dargs_, events, count, stride,
+                       stamps);
   } else {
     void* params[] = {&dargs_, &events, &count, &stride, &stamps};
     HIP_CHECK(hipLaunchCooperativeKernel(reinterpret_cast<void*>(trace_kernel<P, A>), dim3(grid_),

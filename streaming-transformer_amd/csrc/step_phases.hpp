@@ -622,7 +622,10 @@ __device__ __forceinline__ void epilogue(Ctx<P>& c, Phase p, int unit, float s0,
         float co = c.lds.rope_cos[e >> 1], si = c.lds.rope_sin[e >> 1];
         float ra = cast<P>(va * co - vb * si);
         float rb = cast<P>(va * si + vb * co);
-        uint32_t tv = sec == 0 ? a.t_q : a.t_k;
+        // Both offsets are read as uniform values and blended (a select of the two fields
+        // would become a per-lane load from the argument block, waited for with vmcnt(0)).
+        const uint32_t tq = a.t_q, tk = a.t_k;
+        uint32_t tv = tk + (uint32_t)(sec == 0) * (tq - tk);
         c.tstore(tv + i, ep, ra);
         c.tstore(tv + i + 1, ep, rb);
       } else {

@@ -29,7 +29,7 @@ class Backend(enum.IntEnum):
     GRAPH = 1         # staged sequence captured in a hipGraph
     CUBLAS = 2        # vendor GEMV baseline: rocBLAS projections, HIP kernels for the rest
     CUBLAS_GRAPH = 3  # the same captured in a hipGraph
-    FUSED = 4         # one cooperative launch per step
+    FUSED = 4         # one launch per step (plain once the grid is shown co-resident)
     PERSISTENT = 5    # resident kernel + host mailbox
 
 
