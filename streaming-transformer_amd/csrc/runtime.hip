@@ -270,10 +270,19 @@ class Runtime {
   template <class F> auto dispatch(F&& f) {
     using I = std::integral_constant<int, 0>;
     if (args_.attn_regs) {
+      // One instantiation per register attention variant: 16 or 8 16-byte chunks per head
+      // row, or any other count (A = 1, 2, 3).
+      const int chunks = dim_ * (prec_ == kMixed ? 2 : 4) / 16;
+      const int variant = chunks == 16 ? 1 : chunks == 8 ? 2 : 3;
+      auto with = [&](auto P) {
+        if (variant == 1) return f(P, std::integral_constant<int, 1>{});
+        if (variant == 2) return f(P, std::integral_constant<int, 2>{});
+        return f(P, std::integral_constant<int, 3>{});
+      };
       switch (prec_) {
-        case kFp32: return f(std::integral_constant<int, kFp32>{}, std::integral_constant<int, 1>{});
-        case kMixed: return f(std::integral_constant<int, kMixed>{}, std::integral_constant<int, 1>{});
-        default: return f(std::integral_constant<int, kBf16w>{}, std::integral_constant<int, 1>{});
+        case kFp32: return with(std::integral_constant<int, kFp32>{});
+        case kMixed: return with(std::integral_constant<int, kMixed>{});
+        default: return with(std::integral_constant<int, kBf16w>{});
       }
     }
     switch (prec_) {

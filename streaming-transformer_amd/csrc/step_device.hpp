@@ -255,6 +255,12 @@ typedef __attribute__((address_space(3))) float lds_float;
 typedef __attribute__((address_space(3))) v2f lds_v2f;
 typedef __attribute__((address_space(3))) v4f lds_v4f;
 __device__ __forceinline__ lds_float* to_lds(float* p) { return (lds_float*)p; }
+// Load 16 bytes at byte offset off of buffer r (per lane) straight into LDS, no VGPR round
+// trip: dst is the same for every lane of the wave, and lane i's bytes land at dst + 16 i.
+__device__ __forceinline__ void ld16_to_lds(__amdgpu_buffer_rsrc_t r, float* dst, uint32_t off) {
+  typedef __attribute__((address_space(3))) void lds_void;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)to_lds(dst), 16, (int)off, 0, 0, 1);
+}
 // Store two (four) consecutive floats to LDS at p (8- or 16-byte aligned).
 __device__ __forceinline__ void lds_store2(float* p, float2 v) { *(lds_v2f*)p = v2f{v.x, v.y}; }
 __device__ __forceinline__ void lds_store4(float* p, float4 v) { *(lds_v4f*)p = v4f{v.x, v.y, v.z, v.w}; }

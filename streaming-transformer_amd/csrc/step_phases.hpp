@@ -378,7 +378,7 @@ __device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p, int buf, bool r
   float2 nw[kStageNP];
   Own own{0, 0};
   if (p.kind == kAttn) {
-    if constexpr (A == 1) return;
+    if constexpr (A != 0) return;
     ep = c.epoch(ph_index(kQkv, p.layer));
     vec[0] = a.t_q; dst[0] = c.lds.qkv;
     vec[1] = a.t_k; dst[1] = c.lds.qkv + kMaxDim;
@@ -1168,16 +1168,15 @@ __device__ __forceinline__ void compute_final(Ctx<P>& c, const float* xs_buf) {
   }
 }
 
-// A = 1: register attention path; A = 0: LDS path (general head dims).
+// A selects the attention path, one per instantiation: 0 the LDS path (general head dims);
+// the register path with a head row of 1, 2, 3: sixteen, eight, any other number of 16-byte
+// chunks (the host picks A from the head dim).
 template <int P, int A>
 __device__ __forceinline__ void compute(Ctx<P>& c, Phase p, int buf, uint4 (&ring)[kPF]) {
   if (p.kind == kAttn) {
-    if constexpr (A == 1) {
-      constexpr int E = 16 / Traits<P>::kKvBytes;
-      if (c.a.dim == 16 * E) compute_attn_regs<P, 16>(c, p, ring);
-      else if (c.a.dim == 8 * E) compute_attn_regs<P, 8>(c, p, ring);
-      else compute_attn_regs<P, 0>(c, p, ring);
-    }
+    if constexpr (A == 1) compute_attn_regs<P, 16>(c, p, ring);
+    else if constexpr (A == 2) compute_attn_regs<P, 8>(c, p, ring);
+    else if constexpr (A == 3) compute_attn_regs<P, 0>(c, p, ring);
     else compute_attn_lds(c, p, ring);
   } else if (p.kind != kFinal) {
     compute_matvec(c, p, c.lds.xs[buf], c.lds.xres[p.kind == kDown ? 1 : 0], ring);
@@ -1237,7 +1236,6 @@ __global__ __launch_bounds__(kThreads) void phase_kernel(const StepArgs* __restr
 // prefetch the OUT weights instead.
 template <int P>
 __device__ __forceinline__ void load_kv_to_lds(Ctx<P>& c, int layer) {
-  typedef __attribute__((address_space(3))) void lds_void;
   const StepArgs& a = c.a;
   const int nactive = (c.valid + a.chunk - 1) / a.chunk;
   for (int sw = 0; sw < kStreamWaves; sw++) {
@@ -1250,8 +1248,8 @@ __device__ __forceinline__ void load_kv_to_lds(Ctx<P>& c, int layer) {
 #pragma unroll
     for (int j = 0; j < kKB; j++) {
       const uint32_t off = attn_chunk_offset<P>(a, layer, h, ch, c.lane + 64 * j, w.kchunks);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(c.kr, (lds_void*)to_lds(st + 256 * j), 16, (int)off, 0, 0, 1);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(c.vr, (lds_void*)to_lds(st + 256 * (kKB + j)), 16, (int)off, 0, 0, 1);
+      ld16_to_lds(c.kr, st + 256 * j, off);
+      ld16_to_lds(c.vr, st + 256 * (kKB + j), off);
     }
   }
 }
@@ -1291,7 +1289,7 @@ __device__ __forceinline__ void control_loop(Ctx<P>& c, int nph) {
       if (stamps && c.g == 0) put_global(a.stamps, (size_t)kStamps * c.grid * nph, wall_clock64());
       break;
     }
-    if constexpr (A == 1)
+    if constexpr (A != 0)
       if (c.kv_lds && p.kind == kQkv) load_kv_to_lds(c, p.layer);
     // Start polling for the next phase's inputs only once this workgroup's own part of
     // the current phase is done: the producers elsewhere finish at about the same time,
@@ -1305,7 +1303,7 @@ __device__ __forceinline__ void control_loop(Ctx<P>& c, int nph) {
 #endif
     stage_inputs<P, A>(c, phase_of(a, ph + 1), (ph + 1) & 1, true);
     // The attention phase reads the K/V blocks loaded above once the barrier is passed.
-    if (A == 1 && c.kv_lds && p.kind == kQkv) __builtin_amdgcn_s_waitcnt(0);
+    if (A != 0 && c.kv_lds && p.kind == kQkv) __builtin_amdgcn_s_waitcnt(0);
     if (stamps) lstamp(c, ph, 3);
   }
 }
@@ -1334,7 +1332,7 @@ __device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
       // queue empty; OUT is prefetched after attention. (Waves without OUT rows prefetching
       // their GATEUP share here instead was slower: Large 323 -> 329 us, Main 152 -> 161 us.)
       const Phase nxt = phase_of(a, ph + 1);
-      if (!(A == 1 && c.kv_lds && nxt.kind == kAttn)) prefetch(c, nxt, ring);
+      if (!(A != 0 && c.kv_lds && nxt.kind == kAttn)) prefetch(c, nxt, ring);
     }
     if (c.wave >= kWaves - 3) help_stage(c, phase_of(a, ph + 1), (ph + 1) & 1);
     if (stamps) lstamp(c, ph, 7);
@@ -1356,7 +1354,7 @@ __device__ __forceinline__ void forward(Ctx<P>& c) {
   if (a.stamps)
     for (int i = threadIdx.x; i < nst; i += kThreads) (&c.lds.stamps[0][0])[i] = 0u;
   c.split_wide = true;
-  c.kv_lds = A == 1;
+  c.kv_lds = A != 0;
   if (c.wave == 0) control_loop<P, A>(c, nph);
   else stream_loop<P, A>(c, nph);
   if (a.stamps) {
