@@ -6,7 +6,7 @@ and inputs ~ N(0, 1) from seed 3. A "step" is one event through the whole model:
 projection, 12 layers, final norm and score, with the K/V rings carried on the GPU.
 
 Timing: the window is first filled (W-1 events) and warmed (--warmup events), untimed;
-then exactly --steps full-window steps run through the fused backend, one cooperative
+then exactly --steps full-window steps run through the fused backend, one fused-kernel
 launch per step, with a HIP event recorded on the runtime's stream after each launch
 (st_runtime_device_run). `value` is the p50 of those per-step device durations (inputs
 already resident in HBM). The library synchronizes its stream before and after the timed
@@ -426,7 +426,7 @@ def main():
                 extra['scheduled_2000_per_s'][k + '_p50_us'] = round(arrivals[k]['p50_us'], 1)
                 extra['scheduled_2000_per_s'][k + '_p99_us'] = round(arrivals[k]['p99_us'], 1)
             if backend == Backend.FUSED:
-                # Device loop inside one cooperative launch (the reference's deviceTrace).
+                # Device loop inside one launch (the reference's deviceTrace).
                 n = c.window - 1 + 256
                 _, loop = rt.device_trace(events[:n])
                 extra['device_loop_p50_us'] = nearest_rank(loop[c.window - 1:], 0.5)

@@ -156,7 +156,7 @@ int st_runtime_device_trace_noalloc(st_runtime* runtime, const float* device_eve
                                     double* us_per_event, double* per_event_us);
 
 /* Extension (no counterpart in the reference): per-launch device timing. Runs `count`
- * events from a preloaded device copy, one step per launch (FUSED: one cooperative launch
+ * events from a preloaded device copy, one step per launch (FUSED: one fused-kernel launch
  * per event; CUDA/GRAPH: device-to-device staging copy plus the staged step), after a
  * reset if `reset` is nonzero, otherwise continuing the current stream state. A HIP event
  * is recorded on the runtime's stream after every step; per_event_us (may be NULL)

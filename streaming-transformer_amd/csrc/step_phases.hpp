@@ -1380,7 +1380,7 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(const StepArgs* __restr
 }
 
 // Device-only loop over a preloaded trace (the reference's trace_kernel): `count` steps in
-// one cooperative launch (event e at events + e * stride floats), with a wall-clock stamp per
+// one launch (event e at events + e * stride floats), with a wall-clock stamp per
 // step from workgroup 0. Workgroup 0 publishes a step-done word after each FINAL; every
 // workgroup waits for it before the next step writes x.
 template <int P, int A>
@@ -1482,7 +1482,7 @@ __device__ __forceinline__ void snapshot_owned(Ctx<P>& c, unsigned long long t) 
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
 }
 
-// Persistent worker (Backend::PERSISTENT): one cooperative launch serves RUN / RESET / PING /
+// Persistent worker (Backend::PERSISTENT): one resident launch serves RUN / RESET / PING /
 // SNAPSHOT / STOP commands from a host mailbox, following the reference's persistent_kernel
 // (src/cuda/Runtime.cu:58-122) and its ordering contract (docs/transport.md:9-16):
 //  - workgroup 0's control wave acquires the request word (system scope), stages a RUN's
