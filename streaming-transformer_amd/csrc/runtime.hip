@@ -272,11 +272,13 @@ class Runtime {
     if (args_.attn_regs) {
       // One instantiation per register attention variant: 16 or 8 16-byte chunks per head
       // row, or any other count (A = 1, 2, 3).
-      const int chunks = dim_ * (prec_ == kMixed ? 2 : 4) / 16;
-      const int variant = chunks == 16 ? 1 : chunks == 8 ? 2 : 3;
+      const int variant = attn_variant();
+      const bool nt = weights_nt();
       auto with = [&](auto P) {
-        if (variant == 1) return f(P, std::integral_constant<int, 1>{});
-        if (variant == 2) return f(P, std::integral_constant<int, 2>{});
+        if (variant == 1) return nt ? f(P, std::integral_constant<int, 1 | kWeightNt>{})
+                                    : f(P, std::integral_constant<int, 1>{});
+        if (variant == 2) return nt ? f(P, std::integral_constant<int, 2 | kWeightNt>{})
+                                    : f(P, std::integral_constant<int, 2>{});
         return f(P, std::integral_constant<int, 3>{});
       };
       switch (prec_) {
@@ -290,6 +292,20 @@ class Runtime {
       case kMixed: return f(std::integral_constant<int, kMixed>{}, I{});
       default: return f(std::integral_constant<int, kBf16w>{}, I{});
     }
+  }
+  // Register attention variant: 1, 2, 3 for head rows of 16, 8 or another number of 16-byte
+  // chunks (0: the LDS path).
+  int attn_variant() const {
+    if (!args_.attn_regs) return 0;
+    const int chunks = dim_ * (prec_ == kMixed ? 2 : 4) / 16;
+    return chunks == 16 ? 1 : chunks == 8 ? 2 : 3;
+  }
+  // Weights larger than the 256 MB Infinity Cache (MALL) stream with non-temporal loads (bit 2
+  // of the kernels' A parameter, instantiated for variants 1 and 2): they then do not displace
+  // what stays cached across steps. Smaller weight sets stay resident in the cache instead.
+  bool weights_nt() const {
+    const int v = attn_variant();
+    return (size_t)args_.weight_bytes > ((size_t)256 << 20) && (v == 1 || v == 2);
   }
   void check_device_error();
   void sync() { HIP_CHECK(hipStreamSynchronize(stream_)); }
@@ -1473,6 +1489,7 @@ std::string Runtime::info() {
     << ", \"phases_per_step\": " << 5 * c_.layers + 2 << ", \"prefetch_slabs\": " << kPF
     << ", \"attention_chunk\": " << args_.chunk << ", \"weight_arena_bytes\": " << args_.weight_bytes
     << ", \"matvec_implementation\": \"wave64 16-byte buffer loads, register ring, butterfly reduction\""
+    << ", \"weight_loads\": \"" << (weights_nt() ? "non-temporal" : "temporal") << "\""
     << ", \"attention_implementation\": \"" << (args_.attn_regs ? "register" : "LDS-staged")
     << " window chunks, tagged partials combined by the chunk-0 wave\""
     << ", \"transport\": \""

@@ -59,8 +59,10 @@ enum MailboxCommand : int { kCmdRun = 1, kCmdReset = 2, kCmdStop = 3, kCmdPing =
 
 // Buffer-resource dword3 for raw buffer access on gfx9 (32-bit data format).
 constexpr int kRsrcWord3 = 0x00020000;
-// Cache-policy bits for agent-scope coherence (LLVM CPol::SC1).
+// Cache-policy bits for agent-scope coherence (LLVM CPol::SC1) and non-temporal access
+// (CPol::NT).
 constexpr int kSc1 = 16;
+constexpr int kNt = 2;
 
 struct LayerWeights {
   uint32_t norm1, norm2, qkv, out, gateup, down;  // byte offsets into the weight arena
@@ -126,6 +128,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 
 __device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+// A 16-byte weight load. NT marks it non-temporal: weights that exceed the Infinity Cache are
+// streamed without displacing the data that stays cached across steps (K/V rows, the tagged
+// exchange vectors, arguments); weights that fit stay resident in it from step to step.
+template <bool NT>
+__device__ __forceinline__ uint4 ld16w(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, NT ? kNt : 0));
 }
 __device__ __forceinline__ float4 ld16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kSc1));

@@ -44,6 +44,10 @@ struct LdsAll {
   unsigned stamps[kStampPhases][kStamps];  // profiling: low 32 bits of the wall clock
 };
 
+// Bit 2 of a kernel's A parameter: the weights are streamed with non-temporal loads.
+constexpr int kWeightNt = 4;
+constexpr bool weight_nt(int A) { return (A & kWeightNt) != 0; }
+
 template <int P>
 struct Ctx {
   const StepArgs& a;
@@ -378,7 +382,7 @@ __device__ __forceinline__ void stage_inputs(Ctx<P>& c, Phase p, int buf, bool r
   float2 nw[kStageNP];
   Own own{0, 0};
   if (p.kind == kAttn) {
-    if constexpr (A != 0) return;
+    if constexpr ((A & 3) != 0) return;
     ep = c.epoch(ph_index(kQkv, p.layer));
     vec[0] = a.t_q; dst[0] = c.lds.qkv;
     vec[1] = a.t_k; dst[1] = c.lds.qkv + kMaxDim;
@@ -523,13 +527,13 @@ __device__ __forceinline__ void fill_split(Ctx<P>& c) {
   c.split_ready = true;
 }
 
-template <int P>
+template <bool NT, int P>
 __device__ __forceinline__ void prefetch_matvec(Ctx<P>& c, const WaveWork& w, SlabCursor last, uint4 (&ring)[kPF]) {
   if (w.slabs == 0) return;
   SlabCursor cur{w.base, 0};
 #pragma unroll
   for (int j = 0; j < kPF; j++) {
-    ring[j] = ld16(c.wr, (j < w.slabs ? cur : last).offset(c.lane));
+    ring[j] = ld16w<NT>(c.wr, (j < w.slabs ? cur : last).offset(c.lane));
     cur.advance(w);
   }
 }
@@ -584,7 +588,7 @@ __device__ __forceinline__ void load_block(Ctx<P>& c, __amdgpu_buffer_rsrc_t r, 
   for (int j = 0; j < kKB; j++) part[j] = ld16(r, attn_chunk_offset<P>(c.a, layer, h, ch, c.lane + 64 * j, kchunks));
 }
 
-template <int P>
+template <bool NT, int P>
 __device__ __forceinline__ void prefetch(Ctx<P>& c, Phase p, uint4 (&ring)[kPF]) {
   int sw = c.wave - 1;
   if (p.kind == kAttn) {
@@ -598,7 +602,7 @@ __device__ __forceinline__ void prefetch(Ctx<P>& c, Phase p, uint4 (&ring)[kPF])
     int unit0, unit;
     SlabCursor refill, last;
     const WaveWork w = wave_work(c, p, sw, unit0, unit, refill, last);
-    prefetch_matvec(c, w, last, ring);
+    prefetch_matvec<NT>(c, w, last, ring);
   }
 }
 
@@ -653,7 +657,7 @@ __device__ __forceinline__ void epilogue(Ctx<P>& c, Phase p, int unit, float s0,
   }
 }
 
-template <int P>
+template <bool NT, int P>
 __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* xs_buf, const float* xres,
                                                uint4 (&ring)[kPF]) {
   int unit, munit;
@@ -702,7 +706,7 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* 
     for (int j = 0; j < kPF; j++) {
       consume(ring[j]);
       const bool more = pass * kPF + j + kPF < w.slabs;
-      ring[j] = ld16(c.wr, (more ? refill : last).offset(c.lane));
+      ring[j] = ld16w<NT>(c.wr, (more ? refill : last).offset(c.lane));
       if (more) refill.advance(w);
     }
     // At most kPF units finish in one pass (a unit has at least one slab): flush the batch
@@ -1168,18 +1172,19 @@ __device__ __forceinline__ void compute_final(Ctx<P>& c, const float* xs_buf) {
   }
 }
 
-// A selects the attention path, one per instantiation: 0 the LDS path (general head dims);
-// the register path with a head row of 1, 2, 3: sixteen, eight, any other number of 16-byte
-// chunks (the host picks A from the head dim).
+// A selects, one per instantiation, the attention path in its low two bits: 0 the LDS path
+// (general head dims); the register path with a head row of 1, 2, 3: sixteen, eight, any
+// other number of 16-byte chunks. Bit 2 (kWeightNt) makes the weight loads non-temporal.
+// The host picks A from the head dim and the weight bytes.
 template <int P, int A>
 __device__ __forceinline__ void compute(Ctx<P>& c, Phase p, int buf, uint4 (&ring)[kPF]) {
   if (p.kind == kAttn) {
-    if constexpr (A == 1) compute_attn_regs<P, 16>(c, p, ring);
-    else if constexpr (A == 2) compute_attn_regs<P, 8>(c, p, ring);
-    else if constexpr (A == 3) compute_attn_regs<P, 0>(c, p, ring);
+    if constexpr ((A & 3) == 1) compute_attn_regs<P, 16>(c, p, ring);
+    else if constexpr ((A & 3) == 2) compute_attn_regs<P, 8>(c, p, ring);
+    else if constexpr ((A & 3) == 3) compute_attn_regs<P, 0>(c, p, ring);
     else compute_attn_lds(c, p, ring);
   } else if (p.kind != kFinal) {
-    compute_matvec(c, p, c.lds.xs[buf], c.lds.xres[p.kind == kDown ? 1 : 0], ring);
+    compute_matvec<weight_nt(A)>(c, p, c.lds.xs[buf], c.lds.xres[p.kind == kDown ? 1 : 0], ring);
   }
 }
 
@@ -1215,7 +1220,7 @@ __global__ __launch_bounds__(kThreads) void phase_kernel(const StepArgs* __restr
   uint4 ring[kPF];
   fill_rope(c);
   if (c.wave == 0) stage_inputs<P, A>(c, p, 0, false);
-  else prefetch(c, p, ring);
+  else prefetch<weight_nt(A)>(c, p, ring);
   lds_barrier();
   if (p.kind == kFinal) {
     if (c.wave == 0) {
@@ -1289,7 +1294,7 @@ __device__ __forceinline__ void control_loop(Ctx<P>& c, int nph) {
       if (stamps && c.g == 0) put_global(a.stamps, (size_t)kStamps * c.grid * nph, wall_clock64());
       break;
     }
-    if constexpr (A != 0)
+    if constexpr ((A & 3) != 0)
       if (c.kv_lds && p.kind == kQkv) load_kv_to_lds(c, p.layer);
     // Start polling for the next phase's inputs only once this workgroup's own part of
     // the current phase is done: the producers elsewhere finish at about the same time,
@@ -1303,7 +1308,7 @@ __device__ __forceinline__ void control_loop(Ctx<P>& c, int nph) {
 #endif
     stage_inputs<P, A>(c, phase_of(a, ph + 1), (ph + 1) & 1, true);
     // The attention phase reads the K/V blocks loaded above once the barrier is passed.
-    if (A != 0 && c.kv_lds && p.kind == kQkv) __builtin_amdgcn_s_waitcnt(0);
+    if ((A & 3) != 0 && c.kv_lds && p.kind == kQkv) __builtin_amdgcn_s_waitcnt(0);
     if (stamps) lstamp(c, ph, 3);
   }
 }
@@ -1316,7 +1321,7 @@ __device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
   const bool stamps = a.stamps && c.wave == 1 && c.lane == 0;
   fill_split(c);
   uint4 ring[kPF];
-  prefetch(c, phase_of(a, 0), ring);
+  prefetch<weight_nt(A)>(c, phase_of(a, 0), ring);
   for (int ph = 0; ph < nph; ph++) {
     lds_barrier();
     Phase p = phase_of(a, ph);
@@ -1332,7 +1337,7 @@ __device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
       // queue empty; OUT is prefetched after attention. (Waves without OUT rows prefetching
       // their GATEUP share here instead was slower: Large 323 -> 329 us, Main 152 -> 161 us.)
       const Phase nxt = phase_of(a, ph + 1);
-      if (!(A != 0 && c.kv_lds && nxt.kind == kAttn)) prefetch(c, nxt, ring);
+      if (!((A & 3) != 0 && c.kv_lds && nxt.kind == kAttn)) prefetch<weight_nt(A)>(c, nxt, ring);
     }
     if (c.wave >= kWaves - 3) help_stage(c, phase_of(a, ph + 1), (ph + 1) & 1);
     if (stamps) lstamp(c, ph, 7);
@@ -1354,7 +1359,7 @@ __device__ __forceinline__ void forward(Ctx<P>& c) {
   if (a.stamps)
     for (int i = threadIdx.x; i < nst; i += kThreads) (&c.lds.stamps[0][0])[i] = 0u;
   c.split_wide = true;
-  c.kv_lds = A != 0;
+  c.kv_lds = (A & 3) != 0;
   if (c.wave == 0) control_loop<P, A>(c, nph);
   else stream_loop<P, A>(c, nph);
   if (a.stamps) {

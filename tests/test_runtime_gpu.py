@@ -209,6 +209,7 @@ def test_cooperative_grid_limit_and_info():
     assert info['blocks'] == info['environment']['compute_units']
     assert info['legal_cooperative_blocks'] >= info['blocks']
     assert info['fused_launch'] in ('plain', 'cooperative')
+    assert info['weight_loads'] == 'temporal'  # about 17 MB of weights stay in the 256 MB Infinity Cache
     with pytest.raises(RuntimeError, match='occupancy limit'):
         Runtime((c, w, False), RuntimeOptions(backend=Backend.FUSED, blocks=info['legal_cooperative_blocks'] + 1))
     with runtime((c, w, False), Backend.GRAPH, 0) as rt:

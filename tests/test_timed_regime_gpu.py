@@ -76,6 +76,8 @@ def test_large_full_window_matches_oracle(precision):
         storage = WeightStorage.AS_MODEL
     scores, refs, refs32 = [], [], []
     with _runtime((c, w, mixed), Backend.FUSED, weight_dtype=storage) as rt:
+        # Large's weights (430-860 MB) exceed the Infinity Cache: they stream non-temporally.
+        assert rt.info()['weight_loads'] == 'non-temporal'
         for i, e in enumerate(events):
             got, ref = rt.step(e), oracle.step(e)
             ref32 = oracle32.step(e) if oracle32 else None
