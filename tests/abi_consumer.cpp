@@ -1,5 +1,5 @@
 // A C++ consumer of include/st_runtime.h, written the way a maintainer would bind the library
-// into the reference (the Stream::Runtime shim of INTEGRATION.md: status codes turned into
+// into the reference (a Stream::Runtime shim over the C ABI: status codes turned into
 // std::runtime_error(st_last_error()), two-pass sizing of the JSON and trace outputs), driven
 // through the lifecycle checks of the reference's tests/Lifecycle.cu:
 //  - persistent: repeated resets and zero events, position after each step, restart with an

@@ -9,7 +9,7 @@
 - service, scheduled, device and transport modes: exit 0 and the reference's result keys and
   CSV columns;
 - tests/abi_consumer.cpp: the reference's lifecycle checks (tests/Lifecycle.cu) through the
-  ABI as the INTEGRATION.md shim binds it.
+  ABI as a Stream::Runtime shim binds it.
 """
 import csv
 import hashlib

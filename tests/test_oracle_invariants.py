@@ -223,7 +223,7 @@ def test_round_bf16_against_torch():
     ('small', ModelConfig(4, 256, 4, 1024, 64, 256), 160),
     ('main', ModelConfig(8, 512, 8, 2048, 128, 512), 48),
 ])
-def test_float_and_double_accumulation_agree_at_baseline_shapes(name, config, steps):
+def test_float_and_double_accumulation_agree_at_small_and_main_shapes(name, config, steps):
     w = synthetic_checkpoint(config, seed=0)
     events = np.random.default_rng(0).standard_normal((steps, config.features)).astype(np.float32)
     f, d = Oracle(config, w), Oracle(config, w, accumulate='double')

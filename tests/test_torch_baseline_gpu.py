@@ -3,7 +3,7 @@
 bench.py --torch-baseline writes the same step with PyTorch operators in FP32, eager and
 captured in a hipGraph, in a child process (torch brings its own HIP runtime). The test runs
 it on the Small shape and checks that every graph replay equals its eager step exactly and that
-torch's scores agree with this build's runtime on the same events within the reference's FP32
+torch's scores agree with the HIP runtime's on the same events within the reference's FP32
 score gate (1e-5 + 1e-4 |score|, bench/Main.cpp:66).
 """
 import json
