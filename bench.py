@@ -446,6 +446,18 @@ def main():
                 host.append((time.perf_counter() - s) * 1e6)
             extra['persistent_service_p50_us'] = nearest_rank(host, 0.5)
             extra['persistent_service_p99_us'] = nearest_rank(host, 0.99)
+        # The fused backend's host service with mapped staging (RuntimeOptions.mapped: the event
+        # and the score go through mapped pinned memory instead of stream copies).
+        mopts = RuntimeOptions(backend=Backend.FUSED, blocks=0, weight_dtype=opts.weight_dtype, mapped=True)
+        with Runtime((c, weights, mixed), mopts) as rt:
+            rt.device_run(events[:fill], reset=True)
+            host = []
+            for e in events[fill:fill + 256]:
+                s = time.perf_counter()
+                rt.step(e)
+                host.append((time.perf_counter() - s) * 1e6)
+            extra['mapped_host_service_p50_us'] = nearest_rank(host, 0.5)
+            extra['mapped_host_service_p99_us'] = nearest_rank(host, 0.99)
 
     if not args.quick and backend == Backend.FUSED:
         # The reference's default backend (a captured step per event): here the hipGraph holds
