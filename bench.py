@@ -92,8 +92,8 @@ def torch_baseline(c: ModelConfig, weights, events, fill: int, steps: int = 128)
     """The same single-stream step written with PyTorch-ROCm operators in FP32 (the
     reference's bench/torch_bench.py comparison): eager, and captured once in a hipGraph with
     the position held on the device (ring slot, valid-window mask and RoPE angles computed from
-    it). Returns p50 microseconds per step for both and the largest score difference from this
-    build's runtime on the same events (a sanity check, not a parity bar)."""
+    it). Returns p50 microseconds per step for both and the largest score difference from the
+    HIP runtime on the same events (a sanity check, not a parity bar)."""
     import torch
 
     dev = torch.device('cuda')
@@ -380,8 +380,8 @@ def main():
         copy_calibration(args.copy_calibration)
         return
     if args.gpus != 1:
-        print(f'bench.py measures one GPU: the streaming step is a single ordered stream and this '
-              f'build does not shard it (requested --gpus {args.gpus}).', file=sys.stderr)
+        print(f'bench.py measures one GPU: the streaming step is a single ordered stream and the '
+              f'runtime does not shard it (requested --gpus {args.gpus}).', file=sys.stderr)
         sys.exit(2)
 
     c, seed = CONFIGS[args.config]
