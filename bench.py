@@ -13,9 +13,11 @@ already resident in HBM). The library synchronizes its stream before and after t
 launches. One JSON line is printed.
 
 Secondary measurements (skipped with --quick) go under "extra": host-service latency through
-step(), Large in the mixed and bfloat16-weight modes, scheduled arrivals at 2000 events/s, the same step in PyTorch-ROCm (eager and captured), the device loop, the persistent worker, the transport floors (mailbox ping-pong, empty
-launch, empty graph, copy), the vendor GEMV baseline (rocBLAS projections
-in a captured graph) on the same workload, B independent streams over shared weights
+step() (stream copies and mapped staging), Large in the mixed and bfloat16-weight modes,
+scheduled arrivals at 2000 events/s, the same step in PyTorch-ROCm (eager and captured), the
+device loop, the persistent worker, the transport floors (mailbox ping-pong, empty launch,
+empty graph, copy), the vendor GEMV baseline (rocBLAS projections in a captured graph) on the
+same workload, the Main FP32 step across backends, B independent streams over shared weights
 (Main, bfloat16 weights, W=128, B in 1, 16, 64, 256; --batched runs only that), and the Main
 window sweep (W in 32..512, bfloat16 weights and mixed mode).
 
