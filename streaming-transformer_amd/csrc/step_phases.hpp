@@ -39,6 +39,7 @@ struct LdsAll {
   float rope_sin[kMaxDim / 2];
   WaveSplit split[kStreamWaves][kFinal];  // per stream wave and matvec kind (forward only)
   unsigned done[2];                      // stream waves finished with the phase of this parity
+  unsigned refilled[2];                  // DOWN: row waves that have issued all their refills
   unsigned helped[3];                    // epochs of the wide-vector chunks the helper waves staged
   int cmd;                               // persistent worker: the current mailbox command
   unsigned stamps[kStampPhases][kStamps];  // profiling: low 32 bits of the wall clock
@@ -63,13 +64,15 @@ struct Ctx {
   bool split_wide;       // a stream wave polls the odd 1024-piece chunks of wide vectors
   bool kv_lds;           // K/V of each stream wave's first attention item are in its LDS stage
   bool split_ready;      // lds.split holds this wave's matvec shares
+  int phase_parity;      // parity of the phase a stream wave computes (forward)
 #if STAMD_POLL_STAMPS
   int pph = -1;  // phase whose staging stamps the polls record (control wave)
 #endif
 
   __device__ __forceinline__ Ctx(const StepArgs& args, LdsAll& l, int grid_index, int grid_size)
       : a(args), lds(l), g(grid_index), grid(grid_size), lane(lane_id()), wave(wave_id()), t(0), valid(0),
-        slot(0), base(0), dead(false), input(args.input), tagged_input(false), split_wide(false), kv_lds(false), split_ready(false) {
+        slot(0), base(0), dead(false), input(args.input), tagged_input(false), split_wide(false), kv_lds(false), split_ready(false),
+        phase_parity(0) {
     wr = make_rsrc(a.weights, a.weight_bytes);
     kr = make_rsrc(a.keys, a.cache_bytes);
     vr = make_rsrc(a.values, a.cache_bytes);
@@ -717,6 +720,10 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* 
       finished = 0;
     }
   }
+  // Every refill of this wave is issued: the waves without DOWN rows may now queue their
+  // prefetch (streamed weights only; see stream_loop).
+  if (NT && p.kind == kDown && full > 0 && c.lane == 0)
+    __hip_atomic_fetch_add(&c.lds.refilled[c.phase_parity], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   // The last pass: the remaining 1..kPF slabs, no refills.
 #pragma unroll
   for (int j = 0; j < kPF; j++)
@@ -1289,6 +1296,10 @@ __device__ __forceinline__ void control_loop(Ctx<P>& c, int nph) {
     lds_barrier();
     if (stamps) lstamp(c, ph, 0);
     Phase p = phase_of(a, ph);
+    // refilled[ph & 1] counts this phase's DOWN row waves; the other parity's counter was last
+    // read in the previous phase.
+    if (weight_nt(A) && c.lane == 0)
+      __hip_atomic_store(&c.lds.refilled[(ph + 1) & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (p.kind == kFinal) {
       if (c.g == 0) compute_final(c, c.lds.xs[ph & 1]);
       if (stamps && c.g == 0) put_global(a.stamps, (size_t)kStamps * c.grid * nph, wall_clock64());
@@ -1326,6 +1337,7 @@ __device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
     lds_barrier();
     Phase p = phase_of(a, ph);
     if (p.kind == kFinal) break;
+    if constexpr (weight_nt(A)) c.phase_parity = ph & 1;
     compute<P, A>(c, p, ph & 1, ring);
     if (stamps) lstamp(c, ph, 1);
     // Signal before issuing the next phase's prefetch: the issue itself can stall on a
@@ -1337,6 +1349,21 @@ __device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
       // queue empty; OUT is prefetched after attention. (Waves without OUT rows prefetching
       // their GATEUP share here instead was slower: Large 323 -> 329 us, Main 152 -> 161 us.)
       const Phase nxt = phase_of(a, ph + 1);
+      if (weight_nt(A) && p.kind == kDown && c.lds.split[c.wave - 1][kDown].slabs == 0 &&
+          c.lds.split[0][kDown].slabs > kPF) {
+        // Streamed weights, DOWN rows longer than the ring: a wave without DOWN rows waits
+        // (at most 2000 wall-clock ticks, 20 us at 100 MHz; an ordering hint only, on which
+        // no result depends) until the row waves have issued their
+        // refills, so that its QKV prefetch does not sit ahead of them in the CU's memory
+        // queue. Large FP32: 311 -> 307 us.
+        int rows = 0;
+        for (int sw = 0; sw < kStreamWaves; sw++) rows += c.lds.split[sw][kDown].slabs > kPF;
+        const unsigned long long start = wall_clock64();
+        while (__hip_atomic_load(&c.lds.refilled[ph & 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
+                   (unsigned)rows &&
+               wall_clock64() - start < 2000u)
+          __builtin_amdgcn_s_sleep(1);
+      }
       if (!((A & 3) != 0 && c.kv_lds && nxt.kind == kAttn)) prefetch<weight_nt(A)>(c, nxt, ring);
     }
     if (c.wave >= kWaves - 3) help_stage(c, phase_of(a, ph + 1), (ph + 1) & 1);
@@ -1350,6 +1377,7 @@ __device__ __forceinline__ void forward(Ctx<P>& c) {
   const StepArgs& a = c.a;
   const int nph = ph_final(a) + 1;
   if (threadIdx.x == 0) {
+    c.lds.refilled[0] = c.lds.refilled[1] = 0;
     c.lds.done[0] = 0;
     c.lds.done[1] = 0;
     c.lds.helped[0] = c.lds.helped[1] = c.lds.helped[2] = ~0u;
