@@ -39,7 +39,7 @@ struct LdsAll {
   float rope_sin[kMaxDim / 2];
   WaveSplit split[kStreamWaves][kFinal];  // per stream wave and matvec kind (forward only)
   unsigned done[2];                      // stream waves finished with the phase of this parity
-  unsigned refilled[2];                  // DOWN: row waves that have issued all their refills
+  unsigned refilled[2];                  // waves that have issued all their refills in the phase
   unsigned helped[3];                    // epochs of the wide-vector chunks the helper waves staged
   int cmd;                               // persistent worker: the current mailbox command
   unsigned stamps[kStampPhases][kStamps];  // profiling: low 32 bits of the wall clock
@@ -720,9 +720,9 @@ __device__ __forceinline__ void compute_matvec(Ctx<P>& c, Phase p, const float* 
       finished = 0;
     }
   }
-  // Every refill of this wave is issued: the waves without DOWN rows may now queue their
-  // prefetch (streamed weights only; see stream_loop).
-  if (NT && p.kind == kDown && full > 0 && c.lane == 0)
+  // Every refill of this wave is issued: waves that finished earlier may now queue their
+  // next-phase prefetch (streamed weights only; see stream_loop).
+  if (NT && full > 0 && c.lane == 0)
     __hip_atomic_fetch_add(&c.lds.refilled[c.phase_parity], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   // The last pass: the remaining 1..kPF slabs, no refills.
 #pragma unroll
@@ -1296,8 +1296,8 @@ __device__ __forceinline__ void control_loop(Ctx<P>& c, int nph) {
     lds_barrier();
     if (stamps) lstamp(c, ph, 0);
     Phase p = phase_of(a, ph);
-    // refilled[ph & 1] counts this phase's DOWN row waves; the other parity's counter was last
-    // read in the previous phase.
+    // refilled[ph & 1] counts this phase's waves done with their refills; the other parity's
+    // counter was last read in the previous phase.
     if (weight_nt(A) && c.lane == 0)
       __hip_atomic_store(&c.lds.refilled[(ph + 1) & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (p.kind == kFinal) {
@@ -1349,15 +1349,15 @@ __device__ __forceinline__ void stream_loop(Ctx<P>& c, int nph) {
       // queue empty; OUT is prefetched after attention. (Waves without OUT rows prefetching
       // their GATEUP share here instead was slower: Large 323 -> 329 us, Main 152 -> 161 us.)
       const Phase nxt = phase_of(a, ph + 1);
-      if (weight_nt(A) && p.kind == kDown && c.lds.split[c.wave - 1][kDown].slabs == 0 &&
-          c.lds.split[0][kDown].slabs > kPF) {
-        // Streamed weights, DOWN rows longer than the ring: a wave without DOWN rows waits
-        // (at most 2000 wall-clock ticks, 20 us at 100 MHz; an ordering hint only, on which
-        // no result depends) until the row waves have issued their
-        // refills, so that its QKV prefetch does not sit ahead of them in the CU's memory
-        // queue. Large FP32: 311 -> 307 us.
+      if (weight_nt(A) && p.kind != kAttn && c.lds.split[0][p.kind].slabs > kPF) {
+        // Streamed weights, shares longer than the ring: a wave that is done with the phase
+        // waits (at most 2000 wall-clock ticks, 20 us at 100 MHz; an ordering hint only, on
+        // which no result depends) until every wave with refills has issued them, so that its
+        // next-phase prefetch does not sit ahead of them in the CU's memory queue: the waves
+        // without DOWN rows, and in GATEUP the waves with two units against those with three.
+        // Large FP32: 311 -> 303.5 us.
         int rows = 0;
-        for (int sw = 0; sw < kStreamWaves; sw++) rows += c.lds.split[sw][kDown].slabs > kPF;
+        for (int sw = 0; sw < kStreamWaves; sw++) rows += c.lds.split[sw][p.kind].slabs > kPF;
         const unsigned long long start = wall_clock64();
         while (__hip_atomic_load(&c.lds.refilled[ph & 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
                    (unsigned)rows &&
