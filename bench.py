@@ -18,11 +18,12 @@ scheduled arrivals at 2000 events/s, the same step in PyTorch-ROCm (eager and ca
 device loop, the persistent worker, the transport floors (mailbox ping-pong, empty launch,
 empty graph, copy), the vendor GEMV baseline (rocBLAS projections in a captured graph) on the
 same workload, the Main FP32 step across backends, B independent streams over shared weights
-(Main, bfloat16 weights, W=128, B in 1, 16, 64, 256; --batched runs only that), and the Main
+(Main, bfloat16 weights, W=128: the phase-kernel graph at B in 1, 16, 64, 256 and the resident
+fused step per stream at B in 1, 4, 16, 32; --batched runs only those), and the Main
 window sweep (W in 32..512, bfloat16 weights and mixed mode).
 
 Usage: python bench.py [--gpus 1] [--steps 1024] [--warmup 64] [--config large|main|small]
-                       [--precision fp32|bf16w|mixed] [--no-cpu-baseline] [--quick] [--batched]
+                       [--precision fp32|bf16w|mixed] [--no-cpu-baseline] [--quick] [--batched [--resident]]
 """
 from __future__ import annotations
 
@@ -64,20 +65,25 @@ def kv_bytes_per_step(c: ModelConfig, kvb: int, valid: int) -> int:
     return 2 * c.layers * c.width * valid * kvb + 2 * c.layers * c.width * kvb
 
 
-def batched_streams(counts=(1, 16, 64, 256), steps=64, mode='bf16w'):
+def batched_streams(counts=(1, 16, 64, 256), steps=64, mode='bf16w', resident=False):
     """B independent streams over shared weights (st_batch_*): Main architecture, W=128, as in
     the batched configuration, with bfloat16 weights and FP32 K/V (mode 'bf16w') or the
-    reference's mixed mode (FP16 weights and K/V). Each B runs a full window of events
-    (untimed), then `steps` timed steps with a HIP event after each. Algorithmic bytes per
-    step: the weights once plus every stream's K/V window and new rows."""
+    reference's mixed mode (FP16 weights and K/V); `resident`: one launch of the fused step
+    per step, each stream on its own share of the CUs (st_batch_create_resident), else the
+    graph of phase kernels. Each B runs a full window of events (untimed), then `steps` timed
+    steps with a HIP event after each. Algorithmic bytes per step: the weights once plus every
+    stream's K/V window and new rows (the resident kernel reads the weights once per stream,
+    mostly from the Infinity Cache and L2)."""
     c, seed = CONFIGS['main']
     mixed = mode == 'mixed'
     weights = synthetic_checkpoint(c, seed=seed, mixed=mixed)
-    out = {'workload': f'main {mode} batched streams, W={c.window}', 'steps': steps}
+    out = {'workload': f'main {mode} batched streams, W={c.window}', 'steps': steps,
+           'kernel': 'resident fused step per stream' if resident else 'phase-kernel graph'}
     for b in counts:
         rng = np.random.default_rng([seed, 2, b])
         events = rng.standard_normal((c.window + steps, b, c.features), dtype=np.float32)
-        with BatchRuntime((c, weights, mixed), b, WeightStorage.AS_MODEL if mixed else WeightStorage.BF16) as rt:
+        storage = WeightStorage.AS_MODEL if mixed else WeightStorage.BF16
+        with BatchRuntime((c, weights, mixed), b, storage, resident=resident) as rt:
             rt.device_run(events[:c.window])
             mean, per = rt.device_run(events[c.window:])
         p50 = nearest_rank(per, 0.5)
@@ -364,6 +370,8 @@ def main():
                     help='only the PyTorch comparison (FP32, eager and captured); bench.py runs it as a child')
     ap.add_argument('--batched', action='store_true',
                     help='only the batched-streams measurement (B in 1, 16, 64, 256; --steps timed steps each)')
+    ap.add_argument('--resident', action='store_true',
+                    help='with --batched: only the resident rows (B in 1, 4, 16, 32)')
     ap.add_argument('--copy-calibration', type=int, metavar='MIB', default=0,
                     help='only run 8 plain device copies of MIB MiB (reference kernel for HBM counters)')
     args = ap.parse_args()
@@ -374,9 +382,15 @@ def main():
         events = np.random.default_rng([seed, 1]).standard_normal((fill + 128, c.features), dtype=np.float32)
         print(json.dumps(torch_baseline(c, weights, events, fill)), flush=True)
         return
+    if args.batched and args.resident:
+        print(json.dumps({'resident_bf16w': batched_streams(counts=(1, 4, 16, 32), steps=args.steps, resident=True)}),
+              flush=True)
+        return
     if args.batched:
         print(json.dumps({'bf16w': batched_streams(steps=args.steps),
-                          'mixed': batched_streams(steps=args.steps, mode='mixed')}), flush=True)
+                          'mixed': batched_streams(steps=args.steps, mode='mixed'),
+                          'resident_bf16w': batched_streams(counts=(1, 4, 16, 32), steps=args.steps,
+                                                            resident=True)}), flush=True)
         return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
@@ -513,6 +527,7 @@ def main():
                                      for m in ('ping-pong', 'gpu-ping', 'empty', 'empty-graph', 'copy')}
         extra['batched'] = batched_streams()
         extra['batched_mixed'] = batched_streams(mode='mixed')
+        extra['batched_resident'] = batched_streams(counts=(1, 4, 16, 32), resident=True)
         extra['window_sweep'] = window_sweep()
         if args.config == 'large' and args.precision == 'fp32' and backend == Backend.FUSED:
             extra['main_fp32'] = main_backends()

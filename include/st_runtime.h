@@ -231,6 +231,14 @@ int st_probe_json(char* buffer, size_t cap, size_t* needed);
 typedef struct st_batch st_batch;
 int st_batch_create(const st_config* config, int32_t mixed, const st_tensor* tensors, size_t tensor_count,
                     int32_t streams, int32_t weight_dtype, st_batch** out);
+/* Extension, the same batch as one resident launch per step: stream s runs the fused
+ * single-stream step on its own share of the CUs (workgroups [s*per, (s+1)*per), per = the
+ * CU count / streams, a multiple of 8 when at least 8), with its own state and the weights
+ * shared. Each stream's scores and state are bit-identical to a single-stream runtime's (FUSED)
+ * fed the same events. For small batches, which the phase-kernel graph above leaves
+ * launch-bound. streams: 1..32. Every st_batch_* call below applies. */
+int st_batch_create_resident(const st_config* config, int32_t mixed, const st_tensor* tensors, size_t tensor_count,
+                             int32_t streams, int32_t weight_dtype, st_batch** out);
 void st_batch_destroy(st_batch* batch);
 /* inputs: streams*features floats (stream-major); scores: streams floats. */
 int st_batch_step(st_batch* batch, const float* inputs, float* scores);

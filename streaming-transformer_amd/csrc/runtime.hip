@@ -222,10 +222,14 @@ static unsigned long long* trace_scratch_address() {
 
 #include "vendor_path.hpp"
 
+class ResidentBatch;
+
 class Runtime {
  public:
+  // share_weights: use that runtime's weight arena (same config and storage) instead of
+  // building one; it must outlive this runtime.
   Runtime(const st_config& config, bool mixed, const st_tensor* tensors, size_t count,
-          const st_options& options);
+          const st_options& options, const Runtime* share_weights = nullptr);
   ~Runtime();
   float step(const float* input);
   void reset();
@@ -351,10 +355,13 @@ class Runtime {
   const StepArgs* dargs_ = nullptr;
   std::string probe_;
   std::unique_ptr<VendorPath> vendor_;  // CUBLAS / CUBLAS_GRAPH
+
+  // A resident batch launches its streams' steps together and keeps their epochs.
+  friend class ResidentBatch;
 };
 
 Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, size_t count,
-                 const st_options& options)
+                 const st_options& options, const Runtime* share_weights)
     : c_(config), opt_(options) {
   validate_config(c_);
   if (options.idle_seconds <= 0 || options.idle_seconds > 3600 || options.blocks < 0)
@@ -413,7 +420,21 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
     a.attn_regs = pow2 && dim_ >= e && dim_ <= 64 * e && (a.chunk * dim_ * kvb) % 16 == 0 ? 1 : 0;
   }
 
-  build_weights(tensors, count);
+  if (share_weights) {
+    if (share_weights->prec_ != prec_ || share_weights->args_.width_p != a.width_p ||
+        share_weights->args_.ffn_p != a.ffn_p || share_weights->args_.features_p != a.features_p ||
+        share_weights->c_.layers != c_.layers)
+      throw Error(ST_ERR_INVALID, "Shared weights come from a runtime of another shape or storage");
+    const StepArgs& w = share_weights->args_;
+    a.weights = w.weights;
+    a.weight_bytes = w.weight_bytes;
+    a.w_input = w.w_input;
+    a.w_final_norm = w.w_final_norm;
+    a.w_score = w.w_score;
+    for (int l = 0; l < kMaxLayers; l++) a.layer[l] = w.layer[l];
+  } else {
+    build_weights(tensors, count);
+  }
 
   // ---- state
   const size_t kvb = prec_ == kMixed ? 2 : 4;
@@ -1902,7 +1923,7 @@ int st_probe_json(char* buffer, size_t cap, size_t* needed) {
 // ---- batched independent streams (extension)
 
 struct st_batch {
-  std::unique_ptr<stamd::Batch> impl;
+  std::unique_ptr<stamd::BatchBase> impl;
 };
 
 int st_batch_create(const st_config* config, int32_t mixed, const st_tensor* tensors, size_t count, int32_t streams,
@@ -1912,6 +1933,17 @@ int st_batch_create(const st_config* config, int32_t mixed, const st_tensor* ten
     *out = nullptr;
     auto r = std::make_unique<st_batch>();
     r->impl = std::make_unique<stamd::Batch>(*config, mixed != 0, tensors, count, streams, weight_dtype);
+    *out = r.release();
+  });
+}
+
+int st_batch_create_resident(const st_config* config, int32_t mixed, const st_tensor* tensors, size_t count,
+                             int32_t streams, int32_t weight_dtype, st_batch** out) {
+  return guarded([&] {
+    if (!config || !tensors || !out) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    *out = nullptr;
+    auto r = std::make_unique<st_batch>();
+    r->impl = std::make_unique<stamd::ResidentBatch>(*config, mixed != 0, tensors, count, streams, weight_dtype);
     *out = r.release();
   });
 }

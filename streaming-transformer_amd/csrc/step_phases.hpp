@@ -1412,6 +1412,31 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(const StepArgs* __restr
     __hip_atomic_store(a.epoch, c.base + (unsigned)ph_final(a) + 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Several independent streams in one launch: workgroups [s * per, (s + 1) * per) run one step
+// of stream s with that stream's own arguments args[s] (state, tagged arena, epochs; the
+// weight arena may be shared), reading its event at events + s * stride. Every stream runs the
+// fused step unchanged on a grid of `per` workgroups, and the step's results do not depend on
+// the grid size, so each stream's results are bit-identical to the single-stream runtime's.
+// The arguments are one read-only array (a restrict kernel parameter indexed by a uniform
+// value), so their fields load through the scalar cache as in fused_kernel; reached through
+// a loaded pointer they became vector loads queued behind the weight stream (Main 148 ->
+// 251 us). With `per` a multiple of 8, workgroup g of every stream sits on XCD g mod 8
+// (round-robin dispatch), so the streams' reads of the same weight rows meet in one XCD's L2.
+template <int P, int A>
+__global__ __launch_bounds__(kThreads) void fused_streams_kernel(const StepArgs* __restrict__ args, int per,
+                                                                 const float* events, int stride) {
+  const int s = (int)blockIdx.x / per;
+  const StepArgs& a = args[s];
+  __shared__ LdsAll lds;
+  Ctx<P> c(a, lds, (int)blockIdx.x - s * per, per);
+  if (events) c.input = events + (size_t)s * (size_t)stride;
+  c.base = load_epoch(a);
+  c.set_position(load_position(a));
+  forward<P, A>(c);
+  if (c.g == 0 && threadIdx.x == 0)
+    __hip_atomic_store(a.epoch, c.base + (unsigned)ph_final(a) + 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Device-only loop over a preloaded trace (the reference's trace_kernel): `count` steps in
 // one launch (event e at events + e * stride floats), with a wall-clock stamp per
 // step from workgroup 0. Workgroup 0 publishes a step-done word after each FINAL; every

@@ -113,13 +113,14 @@ def library(path: os.PathLike | None = None) -> ctypes.CDLL:
     lib.st_last_error.restype = ctypes.c_char_p
     lib.st_batch_create.argtypes = [ctypes.POINTER(_Config), ctypes.c_int32, ctypes.POINTER(_Tensor),
                                     ctypes.c_size_t, ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(P)]
+    lib.st_batch_create_resident.argtypes = lib.st_batch_create.argtypes
     lib.st_batch_destroy.argtypes = [P]
     lib.st_batch_destroy.restype = None
     lib.st_batch_step.argtypes = [P, F, F]
     lib.st_batch_reset.argtypes = [P, ctypes.c_int32]
     lib.st_batch_snapshot.argtypes = [P, ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64), F, F, F]
     lib.st_batch_device_run.argtypes = [P, F, ctypes.c_size_t, D, D]
-    for name in ('st_batch_create', 'st_batch_step', 'st_batch_reset', 'st_batch_snapshot', 'st_batch_device_run',
+    for name in ('st_batch_create', 'st_batch_create_resident', 'st_batch_step', 'st_batch_reset', 'st_batch_snapshot', 'st_batch_device_run',
                  'st_runtime_create', 'st_runtime_step', 'st_runtime_reset', 'st_runtime_stop',
                  'st_runtime_snapshot', 'st_runtime_device_trace', 'st_runtime_device_trace_noalloc',
                  'st_runtime_device_run', 'st_runtime_phase_times',
@@ -361,9 +362,14 @@ class BatchRuntime:
     """`streams` independent streams over one set of weights (extension; the reference is
     single-stream, docs/Architecture.md:3). Each stream behaves like its own Runtime on the
     same events; a step advances all of them. FP32 checkpoints, weights stored as
-    ``weight_dtype`` (WeightStorage)."""
+    ``weight_dtype`` (WeightStorage).
 
-    def __init__(self, model, streams: int, weight_dtype: int = 0):
+    ``resident=False``: a graph of phase kernels with MFMA projections over the streams
+    (1..256 streams; every stream's results bit-identical for any batch size).
+    ``resident=True``: one launch of the fused step per step, each stream on its own share
+    of the CUs (1..32 streams; every stream's results bit-identical to a FUSED Runtime's)."""
+
+    def __init__(self, model, streams: int, weight_dtype: int = 0, resident: bool = False):
         if isinstance(model, Checkpoint):
             config, tensors, mixed = model.config, model.tensors, model.mixed
         else:
@@ -372,8 +378,10 @@ class BatchRuntime:
         self.streams = int(streams)
         cfg, keep, array = _marshal(config, tensors)
         handle = ctypes.c_void_p()
-        _check(library().st_batch_create(ctypes.byref(cfg), int(bool(mixed)), array, len(array), self.streams,
-                                         int(weight_dtype), ctypes.byref(handle)))
+        create = library().st_batch_create_resident if resident else library().st_batch_create
+        _check(create(ctypes.byref(cfg), int(bool(mixed)), array, len(array), self.streams, int(weight_dtype),
+                      ctypes.byref(handle)))
+        self.resident = bool(resident)
         self._h = handle
         self._scores = np.zeros(self.streams, dtype=np.float32)
 
