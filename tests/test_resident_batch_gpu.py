@@ -27,6 +27,8 @@ SHAPES = {
     'ref-main': ModelConfig(2, 128, 4, 256, 256, 32),
     # head dim 48 (the LDS attention path)
     'dh48': ModelConfig(2, 96, 2, 192, 40, 96),
+    # weights beyond the Infinity Cache: the non-temporal weight-load instantiation
+    'large': ModelConfig(12, 1024, 16, 4096, 512, 1024),
 }
 
 
@@ -53,6 +55,7 @@ def _same_state(a, b):
     ('main', False, WeightStorage.BF16, 4, 40, {2: 17}),
     ('main', False, WeightStorage.AS_MODEL, 16, 12, {}),
     ('dh48', False, WeightStorage.AS_MODEL, 7, 50, {0: 9}),
+    ('large', False, WeightStorage.AS_MODEL, 2, 6, {1: 3}),
 ])
 def test_every_stream_equals_fused_runtime(name, mixed, weights, streams, steps, resets):
     c = SHAPES[name]
