@@ -303,9 +303,13 @@ struct Parser {
         case 't': out += '\t'; break;
         case 'u': {
           unsigned cp = hex4();
-          if (cp >= 0xD800 && cp < 0xDC00 && p + 6 <= s.size() && s[p] == '\\' && s[p + 1] == 'u') {
+          if (cp >= 0xDC00 && cp < 0xE000) fail("unpaired low surrogate");
+          if (cp >= 0xD800 && cp < 0xDC00) {
+            // A high surrogate must be followed by a \u escape holding a low surrogate.
+            if (p + 6 > s.size() || s[p] != '\\' || s[p + 1] != 'u') fail("unpaired high surrogate");
             p += 2;
-            unsigned lo = hex4();
+            const unsigned lo = hex4();
+            if (lo < 0xDC00 || lo >= 0xE000) fail("high surrogate without a low surrogate");
             cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
           }
           utf8(out, cp);
@@ -316,58 +320,98 @@ struct Parser {
     }
     return out;
   }
+  // A number in the JSON grammar: -?(0|[1-9][0-9]*)(.[0-9]+)?([eE][+-]?[0-9]+)?. The whole
+  // token is checked against the grammar before it is converted, so "12-3", "1+" or "01" are
+  // errors, not a prefix that parses.
   Json number() {
-    size_t start = p;
-    bool integral = true;
+    const size_t start = p;
+    auto digits = [&]() {
+      const size_t d0 = p;
+      while (p < s.size() && s[p] >= '0' && s[p] <= '9') p++;
+      return p - d0;
+    };
     if (p < s.size() && s[p] == '-') p++;
-    while (p < s.size() && ((s[p] >= '0' && s[p] <= '9') || s[p] == '.' || s[p] == 'e' || s[p] == 'E' || s[p] == '+' ||
-                            s[p] == '-')) {
-      if (s[p] == '.' || s[p] == 'e' || s[p] == 'E') integral = false;
+    if (p < s.size() && s[p] == '0') {
       p++;
+    } else if (digits() == 0) {
+      fail("bad number");
+    }
+    bool integral = true;
+    if (p < s.size() && s[p] == '.') {
+      p++;
+      integral = false;
+      if (digits() == 0) fail("bad number");
+    }
+    if (p < s.size() && (s[p] == 'e' || s[p] == 'E')) {
+      p++;
+      integral = false;
+      if (p < s.size() && (s[p] == '+' || s[p] == '-')) p++;
+      if (digits() == 0) fail("bad number");
     }
     const std::string t = s.substr(start, p - start);
-    if (t.empty() || t == "-") fail("bad number");
     try {
-      if (integral) {
-        if (t[0] == '-') return Json((long long)std::stoll(t));
-        return Json((unsigned long long)std::stoull(t));
-      }
       size_t used = 0;
-      double v = std::stod(t, &used);
+      if (integral) {
+        if (t[0] == '-') {
+          const long long v = std::stoll(t, &used);
+          if (used == t.size()) return Json(v);
+        } else {
+          const unsigned long long v = std::stoull(t, &used);
+          if (used == t.size()) return Json(v);
+        }
+        fail("bad number");
+      }
+      const double v = std::stod(t, &used);
       if (used != t.size()) fail("bad number");
       return Json(v);
     } catch (const std::out_of_range&) {
-      return Json(std::stod(t));
+      return Json(std::stod(t));  // an integer beyond 64 bits keeps its double value
     } catch (const std::invalid_argument&) {
       fail("bad number");
     }
   }
+  static constexpr int kMaxDepth = 256;  // nesting limit: deeper documents are rejected
+  int depth = 0;
+  struct Nest {
+    Parser& parser;
+    explicit Nest(Parser& q) : parser(q) {
+      if (++parser.depth > kMaxDepth) parser.fail("nesting too deep");
+    }
+    ~Nest() { parser.depth--; }
+  };
   Json value() {
     ws();
     if (p >= s.size()) fail("unexpected end");
     char c = s[p];
-    if (c == '{') {
-      p++;
-      Json o = Json::object();
-      if (take('}')) return o;
-      do {
-        ws();
-        std::string k = string();
-        expect(':');
-        o[k] = value();
-      } while (take(','));
-      expect('}');
-      return o;
+    if (c == '{' || c == '[') {
+      Nest nest(*this);
+      return c == '{' ? object() : array();
     }
-    if (c == '[') {
-      p++;
-      Json a = Json::array();
-      if (take(']')) return a;
-      do a.push_back(value());
-      while (take(','));
-      expect(']');
-      return a;
-    }
+    return scalar(c);
+  }
+  Json object() {
+    p++;
+    Json o = Json::object();
+    if (take('}')) return o;
+    do {
+      ws();
+      std::string k = string();
+      expect(':');
+      o[k] = value();
+    } while (take(','));
+    expect('}');
+    return o;
+  }
+  Json array() {
+    p++;
+    Json a = Json::array();
+    if (take(']')) return a;
+    do a.push_back(value());
+    while (take(','));
+    expect(']');
+    return a;
+  }
+  Json scalar(char c) {
     if (c == '"') return Json(string());
     if (s.compare(p, 4, "true") == 0) {
       p += 4;

@@ -76,3 +76,33 @@ def reference_checkpoint(name: str, target: Path) -> tuple[Path, Path]:
     config_file = target / 'config.json'
     config_file.write_text(json.dumps(config, indent=2) + '\n')
     return target, config_file
+
+
+GATE_METRICS = ('scores', 'keys', 'values', 'hidden')
+
+
+def gate(result, backend, precision, count):
+    """The per-run checks of the reference's correctness gate (bench/gates.py:125-161) on a
+    stream-bench result file."""
+    assert result['mode'] == 'correctness' and result['dropped'] == 0 and result['completed'] == count
+    assert result['backend'] == backend and result['precision'] == precision
+    for metric in GATE_METRICS:
+        e = result[metric]
+        assert e['elements'] > 0 and e['failed'] == 0 and e['nonfinite'] == 0, (metric, e)
+    for metric in ('cache_relative_l2_gate', 'hidden_relative_l2_gate'):
+        assert result[metric]['failed'] == 0 and result[metric]['nonfinite'] == 0
+    assert len(result['provenance']['executable_sha256']) == 64
+
+
+def plant_score_error(oracle_dir: Path, index: int, delta: float) -> None:
+    """Add `delta` to stored score `index` of a stream-sparse-oracle-v1 archive and re-hash it
+    (the planted mistake of the stored-oracle tests goes into the oracle, on the CPU)."""
+    manifest = json.loads((oracle_dir / 'manifest.json').read_text())
+    raw = bytearray((oracle_dir / 'tensors.bin').read_bytes())
+    entry = next(t for t in manifest['tensors'] if t['name'] == 'scores')
+    at = entry['offset'] + 4 * index
+    value = np.frombuffer(bytes(raw[at:at + 4]), dtype='<f4')[0] + np.float32(delta)
+    raw[at:at + 4] = np.float32(value).tobytes()
+    (oracle_dir / 'tensors.bin').write_bytes(bytes(raw))
+    manifest['sha256'] = hashlib.sha256(bytes(raw)).hexdigest()
+    (oracle_dir / 'manifest.json').write_text(json.dumps(manifest))

@@ -3,7 +3,8 @@
 //    sha256("abc")), including inputs that cross the 64-byte block and padding boundaries;
 //  - nearest-rank percentiles (the reference's tests/test_analysis.py:9-12);
 //  - the Errors thresholds at their edges, FP32 and mixed (bench/Main.cpp:57-84);
-//  - JSON round trips and equality as the driver uses them.
+//  - JSON round trips and equality as the driver uses them, and the parser's rejections:
+//    numbers outside the JSON grammar, unpaired surrogates, nesting beyond its limit.
 // With the argument "halves" it prints the FP32 bits of every FP16 bit pattern's decode, one
 // hex word per line, for the Python test to compare with numpy.
 #include "json.hpp"
@@ -78,13 +79,28 @@ int main(int argc, char** argv) {
   expect(Json::parse(j.dump(2)) == j && Json::parse(j.dump()) == j, "dump / parse round trip");
   expect(Json::parse(R"({"x": 1, "y": 1e-05})") == Json::parse(R"({"y": 0.00001, "x": 1})"), "object equality");
   expect(Json::parse("[1]") != Json::parse("[1.5]"), "number inequality");
-  bool threw = false;
-  try {
-    Json::parse("{\"a\": 1,}");
-  } catch (const std::runtime_error&) {
-    threw = true;
-  }
-  expect(threw, "malformed JSON rejected");
+  auto rejected = [](const std::string& text) {
+    try {
+      Json::parse(text);
+    } catch (const std::runtime_error&) {
+      return true;
+    }
+    return false;
+  };
+  expect(rejected("{\"a\": 1,}"), "malformed JSON rejected");
+  // Numbers are checked against the JSON grammar as a whole token: no prefix parses.
+  for (const char* bad : {"12-3", "1+", "01", "-", "1.", ".5", "1e", "1e+", "--1", "[1-2]", "0x10", "+1"})
+    expect(rejected(bad), bad);
+  expect(Json::parse("-0").integer() == 0 && Json::parse("1E+2").number() == 100 && Json::parse("-12").integer() == -12 &&
+             Json::parse("2.5e-1").number() == 0.25,
+         "numbers in the grammar");
+  // Surrogate pairs: a high surrogate needs a following low one; a lone low one is an error.
+  expect(Json::parse(R"("\ud83d\ude00")").str() == "\xF0\x9F\x98\x80", "surrogate pair decodes to U+1F600");
+  for (const char* bad : {R"("\ud83d")", R"("\ud83dx")", R"("\ud83dA")", R"("\ud83d\ud83d")", R"("\ude00")"})
+    expect(rejected(bad), bad);
+  // Nesting depth is bounded.
+  expect(!rejected(std::string(200, '[') + std::string(200, ']')), "200 levels of nesting");
+  expect(rejected(std::string(100000, '[') + std::string(100000, ']')), "100000 levels of nesting rejected");
 
   std::printf("%s: %d failure(s)\n", failures ? "FAILED" : "OK", failures);
   return failures ? 1 : 0;

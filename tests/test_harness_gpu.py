@@ -17,17 +17,15 @@ import json
 import subprocess
 from pathlib import Path
 
-import numpy as np
 import pytest
 
-from harness_layout import reference_checkpoint, reference_fixture
+from harness_layout import gate, plant_score_error, reference_checkpoint, reference_fixture
 
 pytestmark = pytest.mark.gpu
 
 ROOT = Path(__file__).resolve().parent.parent
 BENCH = ROOT / 'streaming-transformer_amd' / 'lib' / 'stream-bench'
 CONSUMER = ROOT / 'tests' / '_build' / 'abi_consumer'
-GATE_METRICS = ('scores', 'keys', 'values', 'hidden')
 
 
 def bench(*args, timeout=240):
@@ -44,18 +42,6 @@ def fixtures(tmp_path_factory):
     return out
 
 
-def gate(result, backend, blocks, precision, count):
-    """The per-run checks of the reference's correctness gate (bench/gates.py:125-161)."""
-    assert result['mode'] == 'correctness' and result['dropped'] == 0 and result['completed'] == count
-    assert result['backend'] == backend and result['precision'] == precision
-    for metric in GATE_METRICS:
-        e = result[metric]
-        assert e['elements'] > 0 and e['failed'] == 0 and e['nonfinite'] == 0, (metric, e)
-    for metric in ('cache_relative_l2_gate', 'hidden_relative_l2_gate'):
-        assert result[metric]['failed'] == 0 and result[metric]['nonfinite'] == 0
-    assert len(result['provenance']['executable_sha256']) == 64
-
-
 VARIANTS = [('cuda', 1), ('cuda', 4), ('graph', 1), ('graph', 4), ('fused', 1), ('fused', 0),
             ('persistent', 1), ('persistent', 4), ('cublas', 4), ('cublas-graph', 4)]
 
@@ -68,7 +54,7 @@ def test_fixture_correctness(fixtures, tmp_path, backend, blocks, precision):
                 '--config', config, '--events', 201, '--output', tmp_path / 'r')
     assert out.returncode == 0, out.stderr[-2000:]
     result = json.loads((tmp_path / 'r.json').read_text())
-    gate(result, backend, blocks, precision, 201)
+    gate(result, backend, precision, 201)
     assert result['expected_source'] == 'fixture'
     # The reset schedule of resets.json was applied: 201 events, reset before event 131.
     assert result['scores']['elements'] == 201 and result['hidden']['elements'] == 201 * 64
@@ -85,19 +71,12 @@ def test_stored_oracle_correctness_and_planted_error(fixtures, tmp_path, precisi
                     '--output', tmp_path / backend)
         assert out.returncode == 0, out.stderr[-2000:]
         result = json.loads((tmp_path / f'{backend}.json').read_text())
-        gate(result, backend, blocks, precision, 300)
+        gate(result, backend, precision, 300)
         assert result['expected_manifest_sha256'] == hashlib.sha256((oracle / 'manifest.json').read_bytes()).hexdigest()
         c = json.loads(config.read_text())
         assert result['keys']['elements'] == 6 * c['layers'] * c['width'] * c['window']  # the 6 stored events
     # The planted mistake goes into the oracle, on the CPU: one score off by 0.05.
-    manifest = json.loads((oracle / 'manifest.json').read_text())
-    raw = bytearray((oracle / 'tensors.bin').read_bytes())
-    scores = np.frombuffer(raw, dtype='<f4', count=300).copy()
-    scores[123] += 0.05
-    raw[:1200] = scores.tobytes()
-    (oracle / 'tensors.bin').write_bytes(bytes(raw))
-    manifest['sha256'] = hashlib.sha256(bytes(raw)).hexdigest()
-    (oracle / 'manifest.json').write_text(json.dumps(manifest))
+    plant_score_error(oracle, 123, 0.05)
     out = bench('--mode', 'correctness', '--backend', 'fused', '--blocks', 0, '--weights', weights, '--config',
                 config, '--events', 300, '--reset-every', 97, '--expected', oracle, '--output', tmp_path / 'planted')
     assert out.returncode == 2, out.stderr[-2000:]
