@@ -14,7 +14,7 @@ import pytest
 
 from oracle.pyoracle import Oracle
 from streamtx import (Backend, BatchRuntime, ModelConfig, Runtime, RuntimeOptions, WeightStorage, numerical,
-                      synthetic_checkpoint)
+                      round_bf16, synthetic_checkpoint)
 
 pytestmark = pytest.mark.gpu
 
@@ -54,6 +54,10 @@ def _same_state(a, b):
     ('small', True, WeightStorage.AS_MODEL, 5, 70, {4: 20}),
     ('main', False, WeightStorage.BF16, 4, 40, {2: 17}),
     ('main', False, WeightStorage.AS_MODEL, 16, 12, {}),
+    # one stream on the whole grid, and the 32-stream limit (8 workgroups per stream): the W = 128
+    # window filled, then 24 full-window steps
+    ('main', False, WeightStorage.BF16, 1, 152, {}),
+    ('main', False, WeightStorage.BF16, 32, 152, {5: 70}),
     ('dh48', False, WeightStorage.AS_MODEL, 7, 50, {0: 9}),
     ('large', False, WeightStorage.AS_MODEL, 2, 6, {1: 3}),
 ])
@@ -103,6 +107,33 @@ def test_every_stream_matches_oracle(name, streams, steps, resets):
             assert state[0] == ref[0]
             for x, y in zip(state[1:], ref[1:]):
                 assert numerical.fp32_strict_failures(x, y, **STRICT) == 0, float(np.abs(x - y).max())
+
+
+@pytest.mark.parametrize('resident_path', [True, False], ids=['resident', 'graph'])
+def test_main_bf16w_single_stream_batch_matches_oracle(resident_path):
+    """Batched Main with bfloat16 weights at B = 1, the configuration the benchmark reports, on
+    the resident kernel and on the phase-kernel graph: the W = 128 window filled, then 24
+    full-window steps, every score and the final state against the FP64-accumulating oracle on
+    the bfloat16-rounded weights (the exact equivalent of bfloat16 storage with FP32 compute)."""
+    c = SHAPES['main']
+    w = synthetic_checkpoint(c, seed=4)
+    oracle = Oracle(c, {k: round_bf16(v) for k, v in w.items()}, accumulate='double', threads=8)
+    steps = c.window + 24
+    events = _events(c, 4, steps, 1)
+    if resident_path:
+        rt = resident((c, w, False), 1, WeightStorage.BF16)
+    else:
+        print('[case] graph batch streams=1 main bf16w', flush=True)
+        rt = BatchRuntime((c, w, False), 1, WeightStorage.BF16)
+    with rt:
+        for i in range(steps):
+            got = rt.step(events[i])[0]
+            ref = oracle.step(events[i, 0])
+            assert numerical.fp32_strict_failures([got], [ref], **STRICT) == 0, (i, got, ref)
+        state, ref = rt.snapshot(0), oracle.snapshot()
+    assert state[0] == ref[0] == steps
+    for x, y in zip(state[1:], ref[1:]):
+        assert numerical.fp32_strict_failures(x, y, **STRICT) == 0, float(np.abs(x - y).max())
 
 
 def test_device_run_equals_stepping_and_reset_is_per_stream():

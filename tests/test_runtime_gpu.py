@@ -112,11 +112,11 @@ def test_fused_matches_oracle_at_shape(name, steps, reset_at):
             refs.append(oracle.step(e))
             refs32.append(oracle32.step(e))
         state = rt.snapshot()
-    fp32bar.check(scores, refs, refs32, 'scores')
+    fp32bar.check(scores, refs, refs32, f'{name} scores')
     ostate, ostate32 = oracle.snapshot(), oracle32.snapshot()
     assert state[0] == ostate[0]
     for name_, a, o, o32 in zip(('keys', 'values', 'hidden'), state[1:], ostate[1:], ostate32[1:]):
-        fp32bar.check(a, o, o32, name_)
+        fp32bar.check(a, o, o32, f'{name} {name_}')
 
 
 @pytest.mark.parametrize('name,steps', [('small', 150), ('main', 140), ('ref-main', 64), ('dh48', 50)])

@@ -2,9 +2,9 @@
 stream lengths, through the C ABI.
 
   - Large (d 1024, 12 layers, 16 heads x 64, FFN 4096, W 512) in FP32, bfloat16-weight and
-    mixed storage: the window is filled (511 events), then 64 full-window steps (32 attention
-    chunks per head, every combine summing 32 partials, the ring wrapping) are compared with
-    the oracle, every step's score and the complete carried state at the end;
+    mixed storage at the configured 4096 events: every score (511 to fill the window, then
+    3585 full-window steps, 32 attention chunks per head, the ring wrapping seven times) and
+    the complete carried state at three points are compared with the oracle;
   - Small (512 events, seed 0) and Main (2048 events, seed 1) FP32 at their configured stream
     lengths on the staged, graph, fused and persistent backends: bit-identical to each other
     and within the FP32 bar of the FP64-accumulating oracle;
@@ -19,6 +19,7 @@ Bars: FP32 |a - r| <= 1e-6 + 1e-5 |r| per score and state element against the FP
 algorithm (tests/fp32bar.py); mixed: numerical.score_errors / mixed_state_passes (policy v3).
 """
 import os
+import threading
 
 import numpy as np
 import pytest
@@ -54,54 +55,88 @@ def _assert_state_strict(state, oracle_state):
         assert bad == 0, (bad, float(np.abs(a - o).max()))
 
 
+def _host_isa():
+    """'v3' (the oracle's AVX2 build, bit-identical results, faster) on hosts that have it."""
+    try:
+        flags = set(open('/proc/cpuinfo').read().split())
+    except OSError:
+        return 'portable'
+    return 'v3' if {'avx2', 'fma', 'bmi2', 'movbe'} <= flags else 'portable'
+
+
+def _oracle_scores(oracles, events, snap_at=()):
+    """Step every oracle through all events, each in its own thread (the C oracle releases the
+    GIL in its calls). Returns the scores [oracle][event] and the snapshots taken after the
+    events in snap_at."""
+    scores = [np.empty(len(events), dtype=np.float64) for _ in oracles]
+    snaps = [{} for _ in oracles]
+
+    def work(k):
+        o = oracles[k]
+        for i, e in enumerate(events):
+            scores[k][i] = o.step(e)
+            if i in snap_at:
+                snaps[k][i] = o.snapshot()
+
+    threads = [threading.Thread(target=work, args=(k,)) for k in range(len(oracles))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    return scores, snaps
+
+
 @pytest.mark.parametrize('precision', ['fp32', 'bf16w', 'mixed'])
-def test_large_full_window_matches_oracle(precision):
+def test_large_configured_stream_matches_oracle(precision):
+    """Large at its configured stream length: 4096 events from seed 3 (511 to fill the window,
+    then 3585 full-window steps with 32 attention chunks per head and the ring wrapping seven
+    times). Every score is compared, and the complete carried state after the last fill event,
+    half way and at the end."""
     c = LARGE
     mixed = precision == 'mixed'
     w = synthetic_checkpoint(c, seed=3, mixed=mixed)
-    fill, timed = c.window - 1, 64
-    events = _events(c, 3, fill + timed)
-    oracle32 = None
+    count = 4096
+    events = _events(c, 3, count)
+    snap_at = (c.window - 2, count // 2 - 1, count - 1)
+    isa = _host_isa()
     if precision == 'bf16w':
         rounded = {k: round_bf16(v) for k, v in w.items()}
-        oracle = Oracle(c, rounded, accumulate='double', threads=THREADS)
-        oracle32 = Oracle(c, rounded, accumulate='float', threads=THREADS)
+        oracles = [Oracle(c, rounded, accumulate=a, threads=THREADS // 2, isa=isa) for a in ('double', 'float')]
         storage = WeightStorage.BF16
     elif mixed:
-        oracle = Oracle(c, w, mixed=True, threads=THREADS)
+        oracles = [Oracle(c, w, mixed=True, threads=THREADS, isa=isa)]
         storage = WeightStorage.AS_MODEL
     else:
-        oracle = Oracle(c, w, accumulate='double', threads=THREADS)
-        oracle32 = Oracle(c, w, accumulate='float', threads=THREADS)
+        oracles = [Oracle(c, w, accumulate=a, threads=THREADS // 2, isa=isa) for a in ('double', 'float')]
         storage = WeightStorage.AS_MODEL
-    scores, refs, refs32 = [], [], []
+    scores, states = np.empty(count, dtype=np.float32), {}
     with _runtime((c, w, mixed), Backend.FUSED, weight_dtype=storage) as rt:
         # Large's weights (430-860 MB) exceed the Infinity Cache: they stream non-temporally.
         assert rt.info()['weight_loads'] == 'non-temporal'
         for i, e in enumerate(events):
-            got, ref = rt.step(e), oracle.step(e)
-            ref32 = oracle32.step(e) if oracle32 else None
-            if i >= fill:
-                scores.append(got)
-                refs.append(ref)
-                refs32.append(ref32)
-        state = rt.snapshot()
-    ostate = oracle.snapshot()
-    print(f'[large {precision}] max |score - oracle| over the {timed} full-window steps: '
-          f'{float(np.max(np.abs(np.array(scores) - np.array(refs)))):.3g}', flush=True)
+            scores[i] = rt.step(e)
+            if i in snap_at:
+                states[i] = rt.snapshot()
+    print(f'[large {precision}] {count} GPU steps done; running the oracle(s) on {THREADS} threads ({isa})',
+          flush=True)
+    refs, snaps = _oracle_scores(oracles, events, snap_at)
+    print(f'[large {precision}] max |score - oracle| over {count} steps: {float(np.max(np.abs(scores - refs[0]))):.3g}',
+          flush=True)
+    for i in snap_at:
+        assert states[i][0] == snaps[0][i][0] == i + 1
     if mixed:
-        assert numerical.score_errors(scores, refs, c.layers)['passed']
-        assert state[0] == ostate[0]
-        assert numerical.mixed_state_passes(*state[1:], *ostate[1:])['passed']
-    else:
-        # FP32 bar, or no worse than the reference's own FP32 algorithm (tests/fp32bar.py).
-        fp32bar.check(scores, refs, refs32, 'scores')
-        ostate32 = oracle32.snapshot()
-        assert state[0] == ostate[0]
-        for name, a, o, o32 in zip(('keys', 'values', 'hidden'), state[1:], ostate[1:], ostate32[1:]):
-            got, ref = fp32bar.check(a, o, o32, name)
-            print(f'[large {precision}] {name}: worst error {got:.3g} x the FP32 bar (float oracle {ref:.3g} x)',
-                  flush=True)
+        assert numerical.score_errors(scores, refs[0], c.layers)['passed']
+        for i in snap_at:
+            assert numerical.mixed_state_passes(*states[i][1:], *snaps[0][i][1:])['passed'], i
+        return
+    # FP32 bar, or no worse than the reference's own FP32 algorithm by both measures
+    # (tests/fp32bar.py); the margins go to gpurun_out/parity_margins.jsonl.
+    m = fp32bar.check(scores, refs[0], refs[1], f'large {precision} scores, {count} events')
+    print(f'[large {precision}] {m}', flush=True)
+    for i in snap_at:
+        for name, a, o, o32 in zip(('keys', 'values', 'hidden'), states[i][1:], snaps[0][i][1:], snaps[1][i][1:]):
+            m = fp32bar.check(a, o, o32, f'large {precision} {name} after event {i}')
+            print(f'[large {precision}] {m}', flush=True)
 
 
 @pytest.mark.parametrize('name,config,seed,steps', [('small', SMALL, 0, 512), ('main', MAIN, 1, 2048)])
