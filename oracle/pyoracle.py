@@ -28,6 +28,8 @@ class _Config(ctypes.Structure):
 
 
 _libs = {}
+# void fn(void* user, const char* name, const float* values, int count)
+_TRACE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float), ctypes.c_int)
 
 
 def build() -> Path:
@@ -48,6 +50,8 @@ def library(isa: str = 'portable') -> ctypes.CDLL:
         lib.so_destroy.argtypes = [ctypes.c_void_p]
         lib.so_step.argtypes = [ctypes.c_void_p, F]
         lib.so_step.restype = ctypes.c_float
+        lib.so_step_trace.argtypes = [ctypes.c_void_p, F, _TRACE_FN, ctypes.c_void_p]
+        lib.so_step_trace.restype = ctypes.c_float
         lib.so_reset.argtypes = [ctypes.c_void_p]
         lib.so_position.argtypes = [ctypes.c_void_p]
         lib.so_position.restype = ctypes.c_uint64
@@ -102,6 +106,19 @@ class Oracle:
     def step(self, event) -> float:
         x = np.ascontiguousarray(event, dtype=np.float32)
         return float(self._lib.so_step(self._h, _fptr(x)))
+
+    def trace_step(self, event):
+        """One step with the per-operation trace (so_step_trace, the reference's CpuTrace):
+        returns (score, {name: float32 array}) with the entries in execution order."""
+        x = np.ascontiguousarray(event, dtype=np.float32)
+        entries = {}
+
+        def take(_user, name, values, count):
+            entries[name.decode()] = np.ctypeslib.as_array(values, shape=(count,)).copy()
+
+        callback = _TRACE_FN(take)
+        score = float(self._lib.so_step_trace(self._h, _fptr(x), callback, None))
+        return score, entries
 
     def reset(self) -> None:
         self._lib.so_reset(self._h)

@@ -9,6 +9,8 @@
  *   oracle_norm     <- Cpu::norm        src/cpu/Cpu.cpp:43-57   (1/sqrt(sum/width + eps), cast)
  *   so_step         <- Cpu::step        src/cpu/Cpu.cpp:59-141  (op order, RoPE :73-83, ring write
  *                                        :91-96, physical-ring attention :97-109, residuals, SwiGLU)
+ *   so_step_trace   <- Cpu::step with a CpuTrace  src/cpu/Cpu.cpp:29-57,64-66,86-133 (entry names
+ *                                        and capture points of linear, norm and the step)
  *   so_reset        <- Cpu::reset       src/cpu/Cpu.cpp:143-148
  *   so_round_half   <- roundHalf        src/runtime/Model.cpp:59-61 (Eigen::half: RNE, overflow to inf)
  *   mixed cast rule <- reference/model.py:1-5 and Math.cast :57-58
@@ -29,6 +31,7 @@
 #include "stream_oracle.h"
 
 #include <math.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
@@ -43,7 +46,17 @@ struct so_state {
   float** w;        /* tensors in canonical order, owned copies */
   float *keys, *values, *hidden;
   float *x, *norm, *q, *k, *v, *attention, *temp, *gate, *up, *logits;
+  so_trace_fn trace; /* per-operation capture (so_step_trace), else NULL */
+  void* trace_user;
 };
+
+/* Report one captured vector as "<prefix><name><suffix>" when tracing. */
+static void emit(const so_state* s, const char* prefix, const char* name, const char* suffix, const float* v, int n) {
+  if (!s->trace) return;
+  char full[96];
+  snprintf(full, sizeof full, "%s%s%s", prefix, name, suffix);
+  s->trace(s->trace_user, full, v, n);
+}
 
 /* ---------------- rounding helpers ---------------- */
 
@@ -132,9 +145,11 @@ static void cast(const so_state* s, float* data, int n) {
   if (s->mixed) for (int i = 0; i < n; i++) data[i] = so_round_half(data[i]);
 }
 
-/* Cpu::linear: output[r] = sum_c W[r,c] * input[c], cast unless final. */
-static void oracle_linear(so_state* s, const float* weight, const float* input, float* output,
-                          int rows, int cols, int final) {
+/* Cpu::linear: output[r] = sum_c W[r,c] * input[c], cast unless final. `prefix` + `name`
+ * names the projection in a trace. */
+static void oracle_linear(so_state* s, const char* prefix, const char* name, const float* weight, const float* input,
+                          float* output, int rows, int cols, int final) {
+  emit(s, prefix, name, ".operand", input, cols);
   if (s->dbl) {
 #pragma omp parallel for num_threads(s->threads) if (s->threads > 1) schedule(static)
     for (int r = 0; r < rows; r++) {
@@ -158,12 +173,16 @@ static void oracle_linear(so_state* s, const float* weight, const float* input, 
       output[r] = sum;
     }
   }
+  emit(s, prefix, name, ".pre_cast", output, rows);
   if (!final) cast(s, output, rows);
+  emit(s, prefix, name, ".linear", output, rows);
 }
 
 /* Cpu::norm */
-static void oracle_norm(so_state* s, const float* input, const float* weight, float* output) {
+static void oracle_norm(so_state* s, const char* prefix, const char* name, const float* input, const float* weight,
+                        float* output) {
   int d = s->c.width;
+  emit(s, prefix, name, ".operand", input, d);
   if (s->dbl) {
     double sum = 0;
     for (int i = 0; i < d; i++) sum += (double)input[i] * input[i];
@@ -175,7 +194,9 @@ static void oracle_norm(so_state* s, const float* input, const float* weight, fl
     float scale = 1.0f / sqrtf(sum / d + s->c.epsilon);
     for (int i = 0; i < d; i++) output[i] = input[i] * scale * weight[i];
   }
+  emit(s, prefix, name, ".pre_cast", output, d);
   cast(s, output, d);
+  emit(s, prefix, name, ".norm", output, d);
 }
 
 so_state* so_create(const so_config* config, int mixed, int accumulate_double,
@@ -278,12 +299,15 @@ float so_step(so_state* s, const float* input) {
   int d = s->dim, width = c->width;
   int slot = (int)(s->position % (uint64_t)c->window);
   int valid = s->position + 1 < (uint64_t)c->window ? (int)(s->position + 1) : c->window;
-  oracle_linear(s, s->w[T_INPUT], input, s->x, width, c->features, 0);
+  oracle_linear(s, "", "input", s->w[T_INPUT], input, s->x, width, c->features, 0);
+  emit(s, "", "input", "", s->x, width);
   for (int l = 0; l < c->layers; l++) {
-    oracle_norm(s, s->x, layer_w(s, l, L_NORM1), s->norm);
-    oracle_linear(s, layer_w(s, l, L_Q), s->norm, s->q, width, width, 0);
-    oracle_linear(s, layer_w(s, l, L_K), s->norm, s->k, width, width, 0);
-    oracle_linear(s, layer_w(s, l, L_V), s->norm, s->v, width, width, 0);
+    char p[32];
+    snprintf(p, sizeof p, "layers.%d.", l);
+    oracle_norm(s, p, "norm1", s->x, layer_w(s, l, L_NORM1), s->norm);
+    oracle_linear(s, p, "q", layer_w(s, l, L_Q), s->norm, s->q, width, width, 0);
+    oracle_linear(s, p, "k", layer_w(s, l, L_K), s->norm, s->k, width, width, 0);
+    oracle_linear(s, p, "v", layer_w(s, l, L_V), s->norm, s->v, width, width, 0);
     /* RoPE on adjacent pairs inside each head, Cpu.cpp:73-83 */
     for (int h = 0; h < c->heads; h++) {
       for (int i = 0; i < d; i += 2) {
@@ -299,6 +323,9 @@ float so_step(so_state* s, const float* input) {
     }
     cast(s, s->q, width);
     cast(s, s->k, width);
+    emit(s, p, "q", "", s->q, width);
+    emit(s, p, "k", "", s->k, width);
+    emit(s, p, "v", "", s->v, width);
     for (int h = 0; h < c->heads; h++) {
       size_t base = ((size_t)l * c->heads + h) * (size_t)c->window * d;
       for (int i = 0; i < d; i++) {
@@ -308,12 +335,14 @@ float so_step(so_state* s, const float* input) {
       oracle_attention(s, l, h, valid);
     }
     cast(s, s->attention, width);
-    oracle_linear(s, layer_w(s, l, L_OUT), s->attention, s->temp, width, width, 0);
+    emit(s, p, "attention", "", s->attention, width);
+    oracle_linear(s, p, "out", layer_w(s, l, L_OUT), s->attention, s->temp, width, width, 0);
     for (int i = 0; i < width; i++) s->x[i] += s->temp[i];
     cast(s, s->x, width);
-    oracle_norm(s, s->x, layer_w(s, l, L_NORM2), s->norm);
-    oracle_linear(s, layer_w(s, l, L_GATE), s->norm, s->gate, c->ffn, width, 0);
-    oracle_linear(s, layer_w(s, l, L_UP), s->norm, s->up, c->ffn, width, 0);
+    emit(s, p, "attention_residual", "", s->x, width);
+    oracle_norm(s, p, "norm2", s->x, layer_w(s, l, L_NORM2), s->norm);
+    oracle_linear(s, p, "gate", layer_w(s, l, L_GATE), s->norm, s->gate, c->ffn, width, 0);
+    oracle_linear(s, p, "up", layer_w(s, l, L_UP), s->norm, s->up, c->ffn, width, 0);
     for (int i = 0; i < c->ffn; i++) {
       if (s->dbl) {
         double g = s->gate[i];
@@ -323,15 +352,26 @@ float so_step(so_state* s, const float* input) {
       }
     }
     cast(s, s->gate, c->ffn);
-    oracle_linear(s, layer_w(s, l, L_DOWN), s->gate, s->temp, width, c->ffn, 0);
+    emit(s, p, "activation", "", s->gate, c->ffn);
+    oracle_linear(s, p, "down", layer_w(s, l, L_DOWN), s->gate, s->temp, width, c->ffn, 0);
     for (int i = 0; i < width; i++) s->x[i] += s->temp[i];
     cast(s, s->x, width);
+    emit(s, p, "hidden", "", s->x, width);
     memcpy(s->hidden + (size_t)l * width, s->x, (size_t)width * sizeof(float));
   }
-  oracle_norm(s, s->x, s->w[T_FINAL_NORM], s->norm);
+  oracle_norm(s, "", "final_norm", s->x, s->w[T_FINAL_NORM], s->norm);
   float score;
-  oracle_linear(s, s->w[T_SCORE], s->norm, &score, 1, width, 1);
+  oracle_linear(s, "", "score", s->w[T_SCORE], s->norm, &score, 1, width, 1);
   s->position++;
+  return score;
+}
+
+float so_step_trace(so_state* s, const float* input, so_trace_fn fn, void* user) {
+  s->trace = fn;
+  s->trace_user = user;
+  const float score = so_step(s, input);
+  s->trace = NULL;
+  s->trace_user = NULL;
   return score;
 }
 

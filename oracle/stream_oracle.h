@@ -45,6 +45,15 @@ so_state* so_create(const so_config* config, int mixed, int accumulate_double,
 void so_destroy(so_state* state);
 /* One event of `features` floats; returns the score (Cpu::step). */
 float so_step(so_state* state, const float* input);
+/* Per-operation trace (the reference's CpuTrace, src/cpu/Cpu.cpp:29-57,64-66,86-133): one
+ * step that also reports every operation and cast boundary to `fn`, in execution order, under
+ * the reference's names: for each projection N ("input", "layers.{l}.q|k|v|out|gate|up|down",
+ * "score") N.operand, N.pre_cast and N.linear; for each norm N ("layers.{l}.norm1|norm2",
+ * "final_norm") N.operand, N.pre_cast and N.norm; and "input", "layers.{l}.q|k|v" (after RoPE
+ * and the cast), "layers.{l}.attention", ".attention_residual", ".activation", ".hidden".
+ * The values pointer is valid only during the call. The step's results are those of so_step. */
+typedef void (*so_trace_fn)(void* user, const char* name, const float* values, int count);
+float so_step_trace(so_state* state, const float* input, so_trace_fn fn, void* user);
 /* Zero K/V/hidden and the position (Cpu::reset, src/cpu/Cpu.cpp:143-148). */
 void so_reset(so_state* state);
 uint64_t so_position(const so_state* state);

@@ -30,6 +30,7 @@ def hipcc() -> str:
 
 HARNESS_DIR = PACKAGE_DIR / 'harness'
 HARNESS = OUTPUT.parent / 'stream-bench'
+DIAGNOSE = OUTPUT.parent / 'stream-diagnose'
 TESTS_DIR = PACKAGE_DIR.parent / 'tests'
 ABI_CONSUMER = TESTS_DIR / '_build' / 'abi_consumer'
 HARNESS_SELFTEST = TESTS_DIR / '_build' / 'harness_selftest'
@@ -47,9 +48,11 @@ def _cxx(source: Path, output: Path, rpath: str) -> None:
 
 
 def build_consumers() -> tuple[Path, Path, Path]:
-    """The benchmark driver (stream-bench, next to the library), and two test programs under
-    tests/_build (test infrastructure): the C++ ABI consumer and the driver's self-test."""
+    """The benchmark driver (stream-bench) and the per-operation diagnostic (stream-diagnose),
+    next to the library, and two test programs under tests/_build (test infrastructure): the
+    C++ ABI consumer and the driver's self-test."""
     _cxx(HARNESS_DIR / 'stream_bench.cpp', HARNESS, '$ORIGIN')
+    _cxx(HARNESS_DIR / 'stream_diagnose.cpp', DIAGNOSE, '$ORIGIN')
     _cxx(TESTS_DIR / 'abi_consumer.cpp', ABI_CONSUMER, '$ORIGIN/../../streaming-transformer_amd/lib')
     _cxx(TESTS_DIR / 'harness_selftest.cpp', HARNESS_SELFTEST, '$ORIGIN/../../streaming-transformer_amd/lib')
     return HARNESS, ABI_CONSUMER, HARNESS_SELFTEST

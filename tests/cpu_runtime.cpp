@@ -5,9 +5,10 @@
 // reset schedules, archives and gates, the scheduled producer/consumer queue, result files and
 // exit codes) runs end to end without a GPU. The product never loads it.
 //
-// Only what the driver calls is provided: create/destroy, step, reset, stop, snapshot,
-// info_json, device_trace and transport_bench (a stub report). A runtime created with
-// max_events > 0 fails its step after that many RUN commands, as the persistent worker does.
+// Only what the drivers call is provided: create/destroy, step, reset, stop, snapshot,
+// info_json, device_trace, trace_step (the oracle's per-operation trace, for stream-diagnose)
+// and transport_bench (a stub report). A runtime created with max_events > 0 fails its step
+// after that many RUN commands, as the persistent worker does.
 #include "st_runtime.h"
 #include "stream_oracle.h"
 
@@ -107,6 +108,43 @@ int st_runtime_device_trace(st_runtime* r, const float* inputs, size_t count, do
   const auto t0 = std::chrono::steady_clock::now();
   for (size_t i = 0; i < count; i++) so_step(r->oracle, inputs + i * (size_t)r->config.features);
   *us_per_event = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count() / (double)count;
+  return ST_OK;
+}
+
+// The oracle's trace in the ABI's layout: names as a JSON object {"name": [offset, count]},
+// values concatenated in execution order.
+int st_runtime_trace_step(st_runtime* r, const float* input, char* names, size_t names_cap, size_t* names_needed,
+                          float* values, size_t values_cap, size_t* values_count) {
+  struct Capture {
+    std::string index = "{";
+    std::vector<float> values;
+  } cap;
+  auto take = [](void* user, const char* name, const float* v, int n) {
+    Capture* c = static_cast<Capture*>(user);
+    if (c->index.size() > 1) c->index += ", ";
+    c->index += "\"" + std::string(name) + "\": [" + std::to_string(c->values.size()) + ", " + std::to_string(n) + "]";
+    c->values.insert(c->values.end(), v, v + n);
+  };
+  if (names_cap == 0 && values_cap == 0) {
+    // Sizes only, no step: the entry layout follows from the configuration. Input projection
+    // f + 3d; per layer 28d + 6F (norms 3d each; q, k, v 3d each plus their rotated values;
+    // attention d; out 3d; attention_residual d; gate and up d + 2F each; activation F; down
+    // F + 2d; hidden d); final norm 3d; score d + 2.
+    const st_config& c = r->config;
+    const size_t d = (size_t)c.width, F = (size_t)c.ffn;
+    *values_count = (size_t)c.features + 7 * d + 2 + (size_t)c.layers * (28 * d + 6 * F);
+    *names_needed = 64 * (10 + 34 * (size_t)c.layers);  // an upper bound: names are under 40 bytes
+    return ST_OK;
+  }
+  if (r->stopped) return fail(ST_ERR_STATE, "Runtime stopped");
+  so_step_trace(r->oracle, input, take, &cap);
+  cap.index += "}";
+  *names_needed = cap.index.size() + 1;
+  *values_count = cap.values.size();
+  if (names_cap < cap.index.size() + 1 || values_cap < cap.values.size())
+    return fail(ST_ERR_INVALID, "trace buffers too small");
+  std::memcpy(names, cap.index.c_str(), cap.index.size() + 1);
+  std::memcpy(values, cap.values.data(), cap.values.size() * sizeof(float));
   return ST_OK;
 }
 
