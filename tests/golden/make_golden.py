@@ -16,8 +16,15 @@ event i is determined by the rows written since the last reset. This script
 keeps those rows and checks, for every event, that rebuilding the cache from
 them reproduces the reference's full tensor bit for bit before writing.
 
-For fixtures/main-{fp32,mixed} (checkpoint and trace, no expected outputs) only
-the checkpoint and trace are kept.
+For fixtures/main-{fp32,mixed} and fixtures/large-{fp32,mixed} (checkpoint and
+trace, no expected outputs) only the checkpoint, trace and reset schedule are kept.
+
+The 30 window variants fixtures/{small,main,large}-w{32,64,128,256,512}-{fp32,mixed}
+hold the same weights as their base checkpoint (scripts/prepare_windows.py:20-23
+refuses any other); only the config's window, the 3W+9-event trace and the reset
+schedule differ. They are kept as windows/<name>/{manifest.json, trace.bin,
+resets.json}, after checking that the variant's tensors.bin is the base's byte for
+byte; tests/harness_layout.py rebuilds each variant from its base checkpoint.
 
 Usage: python tests/golden/make_golden.py [--reference /root/reference]
 """
@@ -111,6 +118,25 @@ def copy_checkpoint(source, target):
         shutil.copyfile(source / name, target / name)
 
 
+def copy_window_variant(source, base, target):
+    """A window variant: its manifest, trace and resets; its tensors must be the base's."""
+    manifest, _ = read_archive(source)  # verifies every hash
+    base_manifest = json.loads((base / 'manifest.json').read_text())
+    if (source / 'tensors.bin').read_bytes() != (base / 'tensors.bin').read_bytes() or \
+            manifest['sha256'] != base_manifest['sha256']:
+        raise ValueError(f'{source.name}: weights differ from {base.name}')
+    config = manifest['config']
+    if {k: v for k, v in config.items() if k != 'window'} != \
+            {k: v for k, v in base_manifest['config'].items() if k != 'window'}:
+        raise ValueError(f'{source.name}: config differs from {base.name} beyond the window')
+    trace = (source / 'trace.bin').read_bytes()
+    if len(trace) != 4 * config['features'] * (3 * config['window'] + 9):
+        raise ValueError(f'{source.name}: trace is not 3W+9 events')
+    target.mkdir(parents=True, exist_ok=True)
+    for name in ('manifest.json', 'trace.bin', 'resets.json'):
+        shutil.copyfile(source / name, target / name)
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument('--reference', type=Path, default=Path('/root/reference'))
@@ -120,9 +146,15 @@ def main():
         copy_checkpoint(fixtures / name, HERE / name)
         compact(fixtures / name, HERE / name)
         print('wrote', HERE / name)
-    for name in ('main-fp32', 'main-mixed'):
+    for name in ('main-fp32', 'main-mixed', 'large-fp32', 'large-mixed'):
         copy_checkpoint(fixtures / name, HERE / name)
         print('wrote', HERE / name)
+    for size in ('small', 'main', 'large'):
+        for window in (32, 64, 128, 256, 512):
+            for mode in ('fp32', 'mixed'):
+                name = f'{size}-w{window}-{mode}'
+                copy_window_variant(fixtures / name, fixtures / f'{size}-{mode}', HERE / 'windows' / name)
+        print('wrote', HERE / 'windows', size)
 
 
 if __name__ == '__main__':

@@ -106,3 +106,42 @@ def plant_score_error(oracle_dir: Path, index: int, delta: float) -> None:
     (oracle_dir / 'tensors.bin').write_bytes(bytes(raw))
     manifest['sha256'] = hashlib.sha256(bytes(raw)).hexdigest()
     (oracle_dir / 'manifest.json').write_text(json.dumps(manifest))
+
+
+def window_fixture(name: str, target: Path) -> tuple[Path, Path]:
+    """tests/golden/windows/<name> (e.g. 'large-w128-mixed') rebuilt as a reference fixture
+    directory: the variant's manifest, trace and resets with its base checkpoint's tensors
+    (the same bytes, checked by make_golden.py). Returns (weights directory, config file)."""
+    source = GOLDEN / 'windows' / name
+    size, _, mode = name.split('-')
+    target.mkdir(parents=True, exist_ok=True)
+    for f in ('manifest.json', 'trace.bin', 'resets.json'):
+        shutil.copyfile(source / f, target / f)
+    shutil.copyfile(GOLDEN / f'{size}-{mode}' / 'checkpoint' / 'tensors.bin', target / 'tensors.bin')
+    config = json.loads((source / 'manifest.json').read_text())['config']
+    config_file = target / 'config.json'
+    config_file.write_text(json.dumps(config, indent=2) + '\n')
+    return target, config_file
+
+
+def adversarial_trace(count: int, features: int, kind: str, seed: int = 123) -> np.ndarray:
+    """The reference's input families (reference/export.py:12-28): N(0,1) events from
+    numpy's default_rng(seed) as little-endian float32, then 'zeros', 'constant' (0.25),
+    'impulses' (1.0 at feature 0 of every 17th event, zeros elsewhere), 'alternating' (every
+    feature +1 on even events, -1 on odd ones), 'repeated' (events cycling through the first
+    7) or 'random' (unchanged)."""
+    x = np.random.default_rng(seed).standard_normal((count, features)).astype('<f4')
+    if kind == 'zeros':
+        x.fill(0)
+    elif kind == 'constant':
+        x.fill(0.25)
+    elif kind == 'impulses':
+        x.fill(0)
+        x[::17, 0] = 1
+    elif kind == 'alternating':
+        x[:] = ((-1.0) ** np.arange(count))[:, None]
+    elif kind == 'repeated':
+        x[:] = x[np.arange(count) % min(count, 7)]
+    elif kind != 'random':
+        raise ValueError(kind)
+    return x
