@@ -12,6 +12,12 @@ launch per step, with a HIP event recorded on the runtime's stream after each la
 already resident in HBM). The library synchronizes its stream before and after the timed
 launches. One JSON line is printed.
 
+Self-check ("self_check" in the line): the state the timed launches leave (position, K/V rings,
+hidden state) and the score of the next event are compared with the C oracle's after the same
+events (float accumulation, the reference's arithmetic) at the reference's bar: FP32
+1e-5 + 1e-4|r| element by element, mixed the policy v3. The same oracle run then gives the CPU
+baseline's timing (skipped together with it by --no-cpu-baseline).
+
 Secondary measurements (skipped with --quick) go under "extra": host-service latency through
 step() (stream copies and mapped staging), Large in the mixed and bfloat16-weight modes,
 scheduled arrivals at 2000 events/s, the same step in PyTorch-ROCm (eager and captured), the
@@ -290,18 +296,32 @@ def matvec_bandwidth(rt, c: ModelConfig, events, wb: int, kvb: int):
 
 
 def host_cpu():
-    """CPU model and hardware thread count of this host (from /proc/cpuinfo)."""
-    model, threads, flags = 'unknown', 0, set()
+    """CPU model (lscpu's model name with family/model/stepping, else /proc/cpuinfo's), hardware
+    thread count and ISA flags of this host."""
+    model, threads, flags, ids = 'unknown', 0, set(), {}
     try:
         for line in Path('/proc/cpuinfo').read_text().splitlines():
-            if line.startswith('model name') and model == 'unknown':
+            key = line.split(':', 1)[0].strip()
+            if key == 'model name' and model == 'unknown':
                 model = line.split(':', 1)[1].strip()
-            elif line.startswith('processor'):
+            elif key == 'processor':
                 threads += 1
-            elif line.startswith('flags') and not flags:
+            elif key == 'flags' and not flags:
                 flags = set(line.split(':', 1)[1].split())
+            elif key in ('cpu family', 'model', 'stepping') and key not in ids:
+                ids[key] = line.split(':', 1)[1].strip()
     except OSError:
         pass
+    try:
+        import subprocess
+        out = subprocess.run(['lscpu'], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith('Model name:'):
+                model = line.split(':', 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if ids:
+        model += f' (family {ids.get("cpu family", "?")}, model {ids.get("model", "?")}, stepping {ids.get("stepping", "?")})'
     return model, threads, flags
 
 
@@ -310,26 +330,52 @@ def nearest_rank(values, q):
     return float(v[max(0, int(math.ceil(q * len(v))) - 1)])
 
 
-def cpu_baseline(c: ModelConfig, weights, mixed, events, fill: int, sample: int, isa: str):
-    """The C oracle (a restatement of the reference CPU step) timed on this host:
-    single thread (the reference default), on `sample` full-window steps, then with an
-    OpenMP split over matvec rows on up to 16 threads. isa: 'v3' (the AVX2 build) or
-    'portable'."""
+def cpu_baseline(c: ModelConfig, weights, mixed, events, upto: int, sample: int, isa: str, check=None):
+    """The C oracle (a restatement of the reference CPU step) on this host's cores.
+
+    Self-check: the oracle (float accumulation, the reference's arithmetic; OpenMP over matvec
+    rows on up to 16 threads) runs the same events as the GPU up to the end of its timed
+    region (events[:upto]); `check` = (the GPU's snapshot there, the GPU's score of
+    events[upto]) is compared with the oracle's at the reference's bar (FP32 1e-5 + 1e-4|r|;
+    mixed, policy v3). Timing: then `sample` further full-window steps single-threaded (the
+    reference default), and `sample` with the 16-thread split. isa: 'v3' (the AVX2 build) or
+    'portable'. Returns (times by thread count, thread count, self-check report)."""
     from oracle.pyoracle import Oracle
+    from streamtx import numerical
     threads_all = min(16, os.cpu_count() or 1)
     oracle = Oracle(c, weights, mixed=mixed, threads=threads_all, isa=isa)
-    for e in events[:fill]:
+    for e in events[:upto]:
         oracle.step(e)
+    report = None
+    if check is not None:
+        (pos, keys, values, hidden), gpu_score = check
+        opos, okeys, ovalues, ohidden = oracle.snapshot()
+        ref_score = oracle.step(events[upto])
+        report = {'events': upto + 1, 'position': int(pos), 'position_matches': int(pos) == int(opos),
+                  'next_score': {'gpu': gpu_score, 'oracle': ref_score, 'abs_diff': abs(gpu_score - ref_score)}}
+        if mixed:
+            st = numerical.mixed_state_passes(keys, values, hidden, okeys, ovalues, ohidden)
+            sc = numerical.score_errors([gpu_score], [ref_score], c.layers)
+            report.update(bar='policy v3 (mixed)', state_failures=len(st['failures']), score_passed=sc['passed'],
+                          passed=bool(st['passed'] and sc['passed'] and report['position_matches']))
+        else:
+            fails = {name: int(numerical.fp32_failures(a, o)) for name, a, o in
+                     (('keys', keys, okeys), ('values', values, ovalues), ('hidden', hidden, ohidden))}
+            fails['score'] = int(numerical.fp32_failures([gpu_score], [ref_score]))
+            report.update(bar='fp32 1e-5 + 1e-4|r| against the float oracle', elements_over_bar=fails,
+                          max_abs_state=float(max(np.abs(a - o).max() for a, o in
+                                                  ((keys, okeys), (values, ovalues), (hidden, ohidden)))),
+                          passed=bool(sum(fails.values()) == 0 and report['position_matches']))
     out = {}
     for threads in (1, threads_all):
         oracle._lib.so_set_threads(oracle._h, threads)
         times = []
-        for e in events[fill:fill + sample]:
+        for e in events[upto - sample:upto]:
             t0 = time.perf_counter()
             oracle.step(e)
             times.append((time.perf_counter() - t0) * 1e6)
         out[threads] = times
-    return out, threads_all
+    return out, threads_all, report
 
 
 def copy_calibration(mib: int) -> None:
@@ -405,7 +451,7 @@ def main():
     weights = synthetic_checkpoint(c, seed=seed, mixed=mixed)
     fill = c.window - 1 + args.warmup
     rng = np.random.default_rng([seed, 1])  # input stream distinct from the weight stream
-    events = rng.standard_normal((fill + args.steps, c.features), dtype=np.float32)
+    events = rng.standard_normal((fill + args.steps + 1, c.features), dtype=np.float32)
     backend = {'fused': Backend.FUSED, 'graph': Backend.GRAPH, 'cuda': Backend.CUDA, 'cublas': Backend.CUBLAS,
                'cublas-graph': Backend.CUBLAS_GRAPH}[args.backend]
     opts = RuntimeOptions(backend=backend, blocks=0,
@@ -421,6 +467,9 @@ def main():
         t0 = time.perf_counter()
         mean_us, per = rt.device_run(events[fill:fill + args.steps])  # exactly --steps launches
         wall = time.perf_counter() - t0
+        # What the timed launches left (position, K/V, hidden) and the next step's score, for the
+        # self-check against the oracle.
+        after_timed = (rt.snapshot(), rt.step(events[fill + args.steps]))
         p50 = nearest_rank(per, 0.5)
         extra['p99_us'] = nearest_rank(per, 0.99)
         extra['mean_us'] = mean_us
@@ -547,18 +596,21 @@ def main():
     extra['mall_resident'] = bytes_step < 256e6
 
     cpu = None
+    self_check = None
     if not args.no_cpu_baseline:
-        sample = {'large': 24, 'main': 80, 'small': 400}[args.config]
-        cfill = c.window - 1
+        sample = min(args.steps, {'large': 24, 'main': 80, 'small': 400}[args.config])
+        upto = fill + args.steps
         model, host_threads, flags = host_cpu()
         isa = 'v3' if {'avx2', 'fma', 'bmi2'} <= flags else 'portable'
-        times, threads_all = cpu_baseline(c, weights if args.precision != 'bf16w' else
-                                          {k: __import__('streamtx').round_bf16(v) for k, v in weights.items()},
-                                          mixed, events, cfill, sample, isa)
+        times, threads_all, self_check = cpu_baseline(
+            c, weights if args.precision != 'bf16w' else
+            {k: __import__('streamtx').round_bf16(v) for k, v in weights.items()},
+            mixed, events, upto, sample, isa, check=after_timed)
         cpu = {'value': nearest_rank(times[1], 0.5), 'unit': 'us per step (p50)', 'cores': 1,
                'kind': 'port',
-               'sample': f'{sample} full-window steps of the same {args.config} {args.precision} workload after a '
-                         f'{cfill}-event fill; C oracle restating src/cpu/Cpu.cpp:59-141, 1 thread, built '
+               'sample': f'{sample} full-window steps of the same {args.config} {args.precision} workload (the last '
+                         f'{sample} timed events, replayed after the oracle has run all {upto + 1}); C oracle '
+                         f'restating src/cpu/Cpu.cpp:59-141, 1 thread, built '
                          f'-O3 {"-march=x86-64-v3 " if isa == "v3" else ""}-ffp-contract=off',
                'cpu_model': model, 'host_threads': host_threads, 'isa': isa,
                'multithread_p50_us': nearest_rank(times[threads_all], 0.5), 'multithread_cores': threads_all}
@@ -575,6 +627,7 @@ def main():
                    'blocks': info['blocks'], 'threads_per_block': info['threads']},
         'roofline': roofline,
         'cpu_baseline': cpu,
+        'self_check': self_check,
         'extra': extra,
     }
     print(json.dumps(line), flush=True)

@@ -142,15 +142,18 @@ int st_runtime_device_trace(st_runtime* runtime, const float* inputs, size_t cou
                             double* us_per_event, double* per_event_us);
 
 /* Extension with no counterpart in the reference: st_runtime_device_trace for callers that
- * cannot allocate device memory (code under stream or graph capture, serving loops, harnesses
- * that forbid hipMalloc). It calls no hipMalloc, hipFree or other allocating routine. FUSED
- * backend only (ST_ERR_INVALID otherwise). device_events holds count*features floats in device
- * memory, row-major and unpadded, which the caller allocated and filled; the call resets the
- * state, runs the events in one launch and writes the mean and (if per_event_us is not NULL)
- * the per-event microseconds like st_runtime_device_trace. The per-step stamps go to a fixed
- * device array of the library with room for ST_NOALLOC_MAX_EVENTS + 1 stamps (8 MiB, held by
- * each GPU the library runs on until the process ends); a larger count is rejected with
- * ST_ERR_INVALID. Every call on one GPU shares that array: calls that overlap on one GPU race. */
+ * cannot allocate device memory (serving loops and harnesses that forbid hipMalloc). It calls
+ * no hipMalloc, hipFree or other allocating routine. It is not for use during stream or graph
+ * capture: it synchronizes the runtime's stream and copies the stamps back with hipMemcpy.
+ * FUSED backend only (ST_ERR_INVALID otherwise). device_events holds count*features floats in
+ * device memory, row-major and unpadded, which the caller allocated and filled; the call resets
+ * the state, runs the events in one launch and writes the mean and (if per_event_us is not
+ * NULL) the per-event microseconds like st_runtime_device_trace. The per-step stamps go to a
+ * fixed device array of the library with room for ST_NOALLOC_MAX_EVENTS + 1 stamps (8 MiB,
+ * held by each GPU the library runs on until the process ends); a larger count is rejected
+ * with ST_ERR_INVALID. Every call on one GPU shares that array; calls on one GPU take turns
+ * (a per-device lock is held from the launch to the stamp readback), so calls from several
+ * threads or runtimes on one GPU serialize instead of racing. */
 #define ST_NOALLOC_MAX_EVENTS ((size_t)1 << 20)
 int st_runtime_device_trace_noalloc(st_runtime* runtime, const float* device_events, size_t count,
                                     double* us_per_event, double* per_event_us);

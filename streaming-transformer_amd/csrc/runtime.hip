@@ -4,6 +4,7 @@
 // the K/V rings, an FP32 scratch arena, the epoch-tagged activation vectors, the
 // device-held position and epoch. Mirrors Stream::Runtime::Impl (src/cuda/Runtime.cu:167-653) behind a C ABI.
 #include "step_phases.hpp"
+#include "mailbox.hpp"
 #include "batch_kernels.hpp"
 #include "diag_kernels.hpp"
 #include "../../include/st_runtime.h"
@@ -130,19 +131,6 @@ struct MappedBuffer {
   }
 };
 
-// Host/device mailbox of the persistent backend (src/cuda/Primitives.cuh:16-23): request,
-// completion and exited words on separate 64-byte lines; only naturally aligned 64-bit
-// loads and stores cross the host/device boundary, no read-modify-write.
-struct alignas(64) Mailbox {
-  alignas(64) unsigned long long request;
-  alignas(64) unsigned long long completion;
-  alignas(64) unsigned long long exited;
-  alignas(64) int32_t command;
-  float score;
-  unsigned long long checksum;
-  uint32_t error;
-};
-
 static void validate_config(const st_config& c) {
   if (c.layers < 1 || c.layers > 16 || c.width < 1 || c.width > 1024 || c.heads < 1 ||
       c.width % c.heads || (c.width / c.heads) % 2 || c.ffn < 1 || c.ffn > 4096 || c.window < 1 ||
@@ -205,6 +193,16 @@ static __device__ __align__(256) unsigned long long trace_scratch[kNoAllocMaxEve
 
 static std::mutex g_scratch_mutex;
 static std::map<int, unsigned long long*> g_scratch_ptr;  // device -> address of trace_scratch there
+// device -> held by an allocation-free trace from its launch to its stamp readback, so that
+// such calls on one GPU (from any runtime or thread) take turns on that GPU's array
+static std::map<int, std::unique_ptr<std::mutex>> g_scratch_use;
+
+static std::mutex& trace_scratch_use(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  std::unique_ptr<std::mutex>& m = g_scratch_use[device];
+  if (!m) m = std::make_unique<std::mutex>();
+  return *m;
+}
 
 // Looks up (once per device) the address of trace_scratch on the current device.
 static unsigned long long* trace_scratch_address() {
@@ -346,9 +344,10 @@ class Runtime {
   DeviceBuffer weights_, keys_, values_, scratch_, tagged_, position_, epoch_dev_, rope_, args_dev_;
   PinnedBuffer host_in_, host_out_;
   MappedBuffer mailbox_, mapped_in_, mapped_snap_, mapped_io_;
-  uint64_t sequence_ = 0;
+  MailboxClient client_;     // host half of the persistent worker's mailbox protocol
   uint64_t epoch_ = 1;       // host copy of the device epoch (the next step's phase-0 epoch)
   unsigned long long* scratch_ptr_ = nullptr;  // this device's trace_scratch (allocation-free trace)
+  int device_ = 0;                             // the device this runtime was created on
   uint64_t runs_done_ = 0;   // RUN commands the persistent worker has completed
   hipStream_t copy_stream_ = nullptr;
   StepArgs args_{};
@@ -389,6 +388,7 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
     throw Error(ST_ERR_DEVICE, std::string("Supported target is gfx950; found ") + prop.gcnArchName);
   cus_ = prop.multiProcessorCount;
   HIP_CHECK(hipDeviceGetAttribute(&wall_khz_, hipDeviceAttributeWallClockRate, device));
+  device_ = device;
   scratch_ptr_ = trace_scratch_address();
   HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   HIP_CHECK(hipStreamCreateWithFlags(&copy_stream_, hipStreamNonBlocking));
@@ -530,9 +530,7 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
     mapped_in_.alloc((size_t)c_.features * 4);
     Mailbox* mb = mailbox();
     Mailbox* dmb = reinterpret_cast<Mailbox*>(mailbox_.dev);
-    sequence_ = options.initial_sequence;
-    mb->request = sequence_;
-    mb->completion = sequence_;
+    client_.attach(mb, options.initial_sequence);
     a.mb_request = &dmb->request;
     a.mb_completion = &dmb->completion;
     a.mb_exited = &dmb->exited;
@@ -951,7 +949,7 @@ void Runtime::restart_worker_rebased() {
   sync();
   rebase_epochs();
   mailbox()->exited = 0;
-  args_.initial_sequence = sequence_;
+  args_.initial_sequence = client_.sequence();
   args_.max_events = opt_.max_events ? opt_.max_events - runs_done_ : 0;
   HIP_CHECK(hipMemcpy(args_dev_.ptr, &args_, sizeof(StepArgs), hipMemcpyHostToDevice));
   start_worker();
@@ -963,43 +961,38 @@ void Runtime::restart_worker_rebased() {
 // STOP. Every command uses one step's worth of epochs.
 void Runtime::command(int cmd) {
   if (!running_) throw Error(ST_ERR_STATE, "Persistent runtime is stopped");
-  Mailbox* mb = mailbox();
-  const uint64_t maximum = std::numeric_limits<uint64_t>::max();
-  if (sequence_ == maximum || (sequence_ == maximum - 1 && cmd != kCmdStop))
-    throw Error(ST_ERR_STATE, "Sequence exhausted; create a new runtime before wraparound");
-  if (__atomic_load_n(&mb->exited, __ATOMIC_ACQUIRE)) {
-    sync();
-    running_ = false;
-    throw Error(ST_ERR_STATE, "Persistent worker exited: finite-event or idle budget reached");
+  try {
+    client_.check(cmd);
+  } catch (const MailboxError& e) {
+    if (e.kind == MailboxError::kExited) {
+      sync();
+      running_ = false;
+    }
+    throw Error(ST_ERR_STATE, e.what());
   }
   // Room for this command and a later STOP; the rebase itself uses one STOP's worth.
-  if (cmd != kCmdStop && epoch_ + 2ull * per_step() > kEpochLimit && sequence_ + 2 < maximum)
+  const uint64_t maximum = std::numeric_limits<uint64_t>::max();
+  if (cmd != kCmdStop && epoch_ + 2ull * per_step() > kEpochLimit && client_.sequence() + 2 < maximum)
     restart_worker_rebased();
   issue(cmd);
   if (cmd == kCmdRun) runs_done_++;
 }
 
 void Runtime::issue(int cmd) {
-  Mailbox* mb = mailbox();
   epoch_ += per_step();
-  mb->command = cmd;
-  __atomic_store_n(&mb->request, ++sequence_, __ATOMIC_RELEASE);
-  const auto start = std::chrono::steady_clock::now();
-  uint64_t polls = 0;
-  while (__atomic_load_n(&mb->completion, __ATOMIC_ACQUIRE) != sequence_) {
-    if (opt_.backoff) std::this_thread::yield();
-    if ((++polls & 0xffff) == 0) {
-      hipError_t status = hipStreamQuery(stream_);
-      if (status != hipErrorNotReady) {
-        HIP_CHECK(status);
-        running_ = false;
-        throw Error(ST_ERR_STATE, "Persistent worker exited before completion");
-      }
-      double waited = std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
-      if (waited > opt_.idle_seconds + 30) throw Error(ST_ERR_STATE, "Persistent response timeout");
-    }
+  // The worker's launch has ended when its stream is idle (a HIP error there is reported).
+  auto finished = [&]() {
+    const hipError_t status = hipStreamQuery(stream_);
+    if (status == hipErrorNotReady) return false;
+    HIP_CHECK(status);
+    return true;
+  };
+  try {
+    client_.issue(cmd, opt_.backoff != 0, opt_.idle_seconds + 30, finished);
+  } catch (const MailboxError& e) {
+    if (e.kind == MailboxError::kExited || e.kind == MailboxError::kExitedBeforeCompletion) running_ = false;
+    throw Error(e.kind == MailboxError::kWatchdog ? ST_ERR_NUMERIC : ST_ERR_STATE, e.what());
   }
-  if (mb->error) throw Error(ST_ERR_NUMERIC, "Device watchdog tripped (error bits " + std::to_string(mb->error) + ")");
 }
 
 // Snapshot (src/cuda/Runtime.cu:548-568). With a live persistent worker, the worker itself
@@ -1134,6 +1127,8 @@ double Runtime::device_trace_noalloc(const float* device_events, size_t count, d
   }
   if (attr.type != hipMemoryTypeDevice) throw Error(ST_ERR_INVALID, "Events must be in device memory");
   unsigned long long* stamps = scratch_ptr_;
+  // One call at a time per GPU on the shared stamp array (launch to readback).
+  std::lock_guard<std::mutex> turn(trace_scratch_use(device_));
   reset();
   reserve_epochs(count);
   const int stride = c_.features;

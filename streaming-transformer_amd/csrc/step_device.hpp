@@ -28,6 +28,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "mailbox.hpp"  // the mailbox commands (kCmd*) shared with the host
+
 namespace stamd {
 
 constexpr int kThreads = 512;
@@ -53,9 +55,6 @@ constexpr int kMaxDim = 1024;
 enum Precision : int { kFp32 = 0, kMixed = 1, kBf16w = 2 };
 enum PhaseKind : int { kInput = 0, kQkv, kAttn, kOut, kGateUp, kDown, kFinal };
 enum ErrorBits : unsigned { kErrPollTimeout = 1u, kErrMailboxTimeout = 2u };
-// Mailbox commands (the reference's Command enum, src/cuda/Primitives.cuh:14), plus the
-// worker's own exit on an exhausted idle budget.
-enum MailboxCommand : int { kCmdRun = 1, kCmdReset = 2, kCmdStop = 3, kCmdPing = 4, kCmdSnapshot = 5, kCmdExit = 64 };
 
 // Buffer-resource dword3 for raw buffer access on gfx9 (32-bit data format).
 constexpr int kRsrcWord3 = 0x00020000;

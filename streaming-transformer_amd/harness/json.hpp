@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <map>
 #include <memory>
 #include <sstream>
@@ -361,14 +362,21 @@ struct Parser {
         }
         fail("bad number");
       }
-      const double v = std::stod(t, &used);
-      if (used != t.size()) fail("bad number");
-      return Json(v);
+      return Json(real(t));
     } catch (const std::out_of_range&) {
-      return Json(std::stod(t));  // an integer beyond 64 bits keeps its double value
+      return Json(real(t));  // an integer beyond 64 bits keeps its double value
     } catch (const std::invalid_argument&) {
       fail("bad number");
     }
+  }
+  // A grammar-checked token as a double: underflow gives the nearest subnormal or zero, a
+  // magnitude beyond the double range is an error.
+  double real(const std::string& t) const {
+    char* end = nullptr;
+    const double v = std::strtod(t.c_str(), &end);
+    if (end != t.c_str() + t.size()) fail("bad number");
+    if (std::isinf(v)) fail("number out of range");
+    return v;
   }
   static constexpr int kMaxDepth = 256;  // nesting limit: deeper documents are rejected
   int depth = 0;

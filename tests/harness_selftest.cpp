@@ -6,7 +6,8 @@
 //  - JSON round trips and equality as the driver uses them, and the parser's rejections:
 //    numbers outside the JSON grammar, unpaired surrogates, nesting beyond its limit.
 // With the argument "halves" it prints the FP32 bits of every FP16 bit pattern's decode, one
-// hex word per line, for the Python test to compare with numpy.
+// hex word per line, for the Python test to compare with numpy; with "fuzz N" it feeds N
+// mutated documents to the JSON parser (for the sanitizer builds).
 #include "json.hpp"
 #include "metrics.hpp"
 #include "model.hpp"
@@ -27,7 +28,48 @@ static void expect(bool ok, const char* what) {
   }
 }
 
+// Random mutations of valid documents (byte flips, truncations, insertions of structural
+// characters) through the parser: each must parse or throw std::runtime_error; under the
+// address and undefined-behaviour sanitizers any out-of-bounds read or overflow aborts.
+static int fuzz(unsigned rounds) {
+  const std::vector<std::string> seeds{
+      R"({"version": 1, "config": {"layers": 2, "epsilon": 1e-05}, "tensors": [{"name": "x", "offset": 0}]})",
+      R"([1, -2.5e+3, "a\u00e9\ud83d\ude00", true, false, null, {"k": [[], {}]}])",
+      R"({"state_events": [0, 64, 128], "sha256": "00ff", "n": 18446744073709551615})"};
+  uint64_t x = 0x9E3779B97F4A7C15ull;
+  auto next = [&]() {
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    return x;
+  };
+  const char alphabet[] = "{}[],:\"\\0123456789.eE+-tfnu ";
+  unsigned parsed = 0;
+  for (unsigned r = 0; r < rounds; r++) {
+    std::string doc = seeds[next() % seeds.size()];
+    const unsigned edits = 1 + next() % 4;
+    for (unsigned e = 0; e < edits && !doc.empty(); e++) {
+      const size_t at = next() % doc.size();
+      switch (next() % 4) {
+        case 0: doc[at] = alphabet[next() % (sizeof alphabet - 1)]; break;
+        case 1: doc.erase(at, 1 + next() % 3); break;
+        case 2: doc.insert(at, 1, alphabet[next() % (sizeof alphabet - 1)]); break;
+        default: doc.resize(at); break;
+      }
+    }
+    try {
+      const Json j = Json::parse(doc);
+      (void)j.dump(2);
+      parsed++;
+    } catch (const std::runtime_error&) {
+    }
+  }
+  std::printf("fuzz: %u rounds, %u parsed\n", rounds, parsed);
+  return 0;
+}
+
 int main(int argc, char** argv) {
+  if (argc > 2 && std::string(argv[1]) == "fuzz") return fuzz((unsigned)std::stoul(argv[2]));
   if (argc > 1 && std::string(argv[1]) == "halves") {
     for (unsigned h = 0; h < 65536; h++) {
       const float f = half_to_float((uint16_t)h);
@@ -94,6 +136,11 @@ int main(int argc, char** argv) {
   expect(Json::parse("-0").integer() == 0 && Json::parse("1E+2").number() == 100 && Json::parse("-12").integer() == -12 &&
              Json::parse("2.5e-1").number() == 0.25,
          "numbers in the grammar");
+  // Doubles beyond the range are errors; underflow rounds to a subnormal or zero; integers
+  // beyond 64 bits keep their double value.
+  expect(rejected("1e99999") && rejected("[-1.5e400]"), "overflowing numbers rejected");
+  expect(Json::parse("1e-400").number() == 0.0 && Json::parse("4.9e-324").number() > 0.0, "underflow");
+  expect(Json::parse("123456789012345678901234567890").number() == 123456789012345678901234567890.0, "wide integer");
   // Surrogate pairs: a high surrogate needs a following low one; a lone low one is an error.
   expect(Json::parse(R"("\ud83d\ude00")").str() == "\xF0\x9F\x98\x80", "surrogate pair decodes to U+1F600");
   for (const char* bad : {R"("\ud83d")", R"("\ud83dx")", R"("\ud83dA")", R"("\ud83d\ud83d")", R"("\ude00")"})
