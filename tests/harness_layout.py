@@ -12,8 +12,11 @@ from __future__ import annotations
 
 import hashlib
 import json
+import os
 import shutil
+import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 import numpy as np
@@ -23,6 +26,29 @@ sys.path.insert(0, str(HERE / 'golden'))
 from make_golden import rebuild_cache  # noqa: E402
 
 GOLDEN = HERE / 'golden'
+ROOT = HERE.parent
+STAND_IN = HERE / '_build' / 'cpu_runtime' / 'libstamd.so'
+
+
+def build_stand_in() -> Path:
+    """tests/cpu_runtime.cpp over the C oracle, built as libstamd.so for the driver's CPU tests.
+
+    Built under a private name and renamed into place, so test processes running at once never
+    load a partly written library.
+    """
+    STAND_IN.parent.mkdir(parents=True, exist_ok=True)
+    fd, tmp = tempfile.mkstemp(prefix='libstamd.', suffix='.so.tmp', dir=STAND_IN.parent)
+    os.close(fd)
+    try:
+        subprocess.run(['g++', '-O2', '-std=c++17', '-shared', '-fPIC', '-fopenmp', f'-I{ROOT / "include"}',
+                        f'-I{ROOT / "oracle"}', '-o', tmp, str(HERE / 'cpu_runtime.cpp'), '-x', 'c',
+                        '-ffp-contract=off', str(ROOT / 'oracle' / 'stream_oracle.c'), '-lm'],
+                       check=True, capture_output=True, text=True)
+        os.replace(tmp, STAND_IN)
+    finally:
+        if os.path.exists(tmp):
+            os.unlink(tmp)
+    return STAND_IN
 
 
 def write_archive(directory: Path, tensors: dict, **fields) -> None:

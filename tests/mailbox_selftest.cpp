@@ -48,7 +48,13 @@ class FakeWorker {
       : mb_(mb), event_(event), features_(features), o_(o) {
     thread_ = std::thread([this] { loop(); });
   }
-  ~FakeWorker() { join(); }
+  ~FakeWorker() {
+    release();
+    join();
+  }
+  // Ends the idle wait at once (a worker that never answers stays until released, however
+  // slowly the host reaches its own timeout check).
+  void release() { released_.store(true, std::memory_order_release); }
   void join() {
     if (thread_.joinable()) thread_.join();
   }
@@ -68,7 +74,9 @@ class FakeWorker {
           cmd = __atomic_load_n(&mb_->command, __ATOMIC_RELAXED);
           break;
         }
-        if (std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count() >= o_.idle_seconds) break;
+        if (released_.load(std::memory_order_acquire) ||
+            std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count() >= o_.idle_seconds)
+          break;
         std::this_thread::yield();
       }
       if (cmd == kCmdExit) break;
@@ -117,6 +125,7 @@ class FakeWorker {
   WorkerOptions o_;
   uint64_t position_ = 0;
   std::atomic<bool> done_{false};
+  std::atomic<bool> released_{false};
   std::thread thread_;
 };
 
@@ -224,11 +233,12 @@ int main() {
     h.client.attach(mb, 0);
     WorkerOptions o{0};
     o.answer = false;
-    o.idle_seconds = 1.0;
+    o.idle_seconds = 600.0;  // stays until released below
     FakeWorker w(mb, event.data(), 32, o);
     h.worker = &w;
     expect(h.fails_with(kCmdRun) == MailboxError::kTimeout, "an unanswered command times out");
-    w.join();  // the worker leaves after its idle budget
+    w.release();
+    w.join();
   }
   {  // a launch that ends without answering
     Host h;

@@ -80,11 +80,8 @@ def test_oracle_operations_meet_their_closed_forms(tmp_path, name):
 def cpu_env():
     """The CPU stand-in runtime as libstamd.so (built by test_harness's fixture when run there)."""
     import os
-    lib = ROOT / 'tests' / '_build' / 'cpu_runtime' / 'libstamd.so'
-    lib.parent.mkdir(parents=True, exist_ok=True)
-    subprocess.run(['g++', '-O2', '-std=c++17', '-shared', '-fPIC', '-fopenmp', f'-I{ROOT / "include"}',
-                    f'-I{ROOT / "oracle"}', '-o', str(lib), str(ROOT / 'tests' / 'cpu_runtime.cpp'), '-x', 'c',
-                    '-ffp-contract=off', str(ROOT / 'oracle' / 'stream_oracle.c'), '-lm'], check=True)
+    from harness_layout import build_stand_in
+    lib = build_stand_in()
     if not DIAGNOSE.exists():
         from streamtx import build
         build.build_consumers()

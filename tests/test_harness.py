@@ -22,7 +22,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from harness_layout import gate, plant_score_error, reference_checkpoint, reference_fixture
+from harness_layout import build_stand_in, gate, plant_score_error, reference_checkpoint, reference_fixture
 
 ROOT = Path(__file__).resolve().parent.parent
 BENCH = ROOT / 'streaming-transformer_amd' / 'lib' / 'stream-bench'
@@ -130,11 +130,7 @@ CPU_RUNTIME = ROOT / 'tests' / '_build' / 'cpu_runtime' / 'libstamd.so'
 def cpu_env(built):
     """Environment that loads tests/cpu_runtime.cpp (over the C oracle) as libstamd.so."""
     import os
-    CPU_RUNTIME.parent.mkdir(parents=True, exist_ok=True)
-    cmd = ['g++', '-O2', '-std=c++17', '-shared', '-fPIC', '-fopenmp', f'-I{ROOT / "include"}',
-           f'-I{ROOT / "oracle"}', '-o', str(CPU_RUNTIME), str(ROOT / 'tests' / 'cpu_runtime.cpp'),
-           '-x', 'c', '-ffp-contract=off', str(ROOT / 'oracle' / 'stream_oracle.c'), '-lm']
-    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    build_stand_in()
     env = dict(os.environ)
     env['LD_LIBRARY_PATH'] = f'{CPU_RUNTIME.parent}:' + env.get('LD_LIBRARY_PATH', '')
     return env

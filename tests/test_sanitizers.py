@@ -71,12 +71,8 @@ def test_json_and_selftest_under_asan():
 
 @pytest.fixture(scope='module')
 def stand_in():
-    lib = ROOT / 'tests' / '_build' / 'cpu_runtime' / 'libstamd.so'
-    lib.parent.mkdir(parents=True, exist_ok=True)
-    subprocess.run(['g++', '-O2', '-std=c++17', '-shared', '-fPIC', '-fopenmp', f'-I{ROOT / "include"}',
-                    f'-I{ROOT / "oracle"}', '-o', str(lib), str(ROOT / 'tests' / 'cpu_runtime.cpp'), '-x', 'c',
-                    '-ffp-contract=off', str(ROOT / 'oracle' / 'stream_oracle.c'), '-lm'], check=True)
-    return lib
+    from harness_layout import build_stand_in
+    return build_stand_in()
 
 
 def driver(flavour, stand_in):
