@@ -9,15 +9,15 @@ two measures against the FP64 referee:
   - its worst normalized error, max_i |a_i - r_i| / bar_i, is no larger than the float
     oracle's (or within the bar);
   - its count of elements over the bar is no larger than the float oracle's count.
-Both figures, for the GPU and for the float oracle, are returned (and appended to
-gpurun_out/parity_margins.jsonl when that folder exists) so that a run records its margins.
+Both figures, for the GPU and for the float oracle, are returned, and appended as JSON lines to
+the file named by STAMD_PARITY_MARGINS when that variable is set, so that a run can record its
+margins.
 """
 import json
-from pathlib import Path
+import os
 
 import numpy as np
 
-MARGINS = Path(__file__).resolve().parent.parent / 'gpurun_out' / 'parity_margins.jsonl'
 
 
 def bar(reference, atol=1e-6, rtol=1e-5):
@@ -42,8 +42,9 @@ def worst(actual, reference):
 
 
 def record(entry: dict) -> None:
-    if MARGINS.parent.is_dir():
-        with open(MARGINS, 'a') as f:
+    path = os.environ.get('STAMD_PARITY_MARGINS')
+    if path:
+        with open(path, 'a') as f:
             f.write(json.dumps(entry) + '\n')
 
 
