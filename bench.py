@@ -29,7 +29,8 @@ fused step per stream at B in 1, 4, 16, 32; --batched runs only those), and the 
 window sweep (W in 32..512, bfloat16 weights and mixed mode).
 
 Usage: python bench.py [--gpus 1] [--steps 1024] [--warmup 64] [--config large|main|small]
-                       [--precision fp32|bf16w|mixed] [--no-cpu-baseline] [--quick] [--batched [--resident]]
+                       [--precision fp32|bf16w|mixed] [--no-cpu-baseline] [--quick]
+                       [--batched [--resident | --eager [--streams 1,16,64,256]]]
 """
 from __future__ import annotations
 
@@ -71,12 +72,13 @@ def kv_bytes_per_step(c: ModelConfig, kvb: int, valid: int) -> int:
     return 2 * c.layers * c.width * valid * kvb + 2 * c.layers * c.width * kvb
 
 
-def batched_streams(counts=(1, 16, 64, 256), steps=64, mode='bf16w', resident=False):
+def batched_streams(counts=(1, 16, 64, 256), steps=64, mode='bf16w', resident=False, eager=False):
     """B independent streams over shared weights (st_batch_*): Main architecture, W=128, as in
     the batched configuration, with bfloat16 weights and FP32 K/V (mode 'bf16w') or the
     reference's mixed mode (FP16 weights and K/V); `resident`: one launch of the fused step
     per step, each stream on its own share of the CUs (st_batch_create_resident), else the
-    graph of phase kernels. Each B runs a full window of events (untimed), then `steps` timed
+    graph of phase kernels (`eager`: its kernels launched directly instead of the graph replay,
+    for kernel traces). Each B runs a full window of events (untimed), then `steps` timed
     steps with a HIP event after each. Algorithmic bytes per step: the weights once plus every
     stream's K/V window and new rows (the resident kernel reads the weights once per stream,
     mostly from the Infinity Cache and L2)."""
@@ -84,12 +86,15 @@ def batched_streams(counts=(1, 16, 64, 256), steps=64, mode='bf16w', resident=Fa
     mixed = mode == 'mixed'
     weights = synthetic_checkpoint(c, seed=seed, mixed=mixed)
     out = {'workload': f'main {mode} batched streams, W={c.window}', 'steps': steps,
-           'kernel': 'resident fused step per stream' if resident else 'phase-kernel graph'}
+           'kernel': 'resident fused step per stream' if resident else
+           'phase kernels, eager launches' if eager else 'phase-kernel graph'}
     for b in counts:
         rng = np.random.default_rng([seed, 2, b])
         events = rng.standard_normal((c.window + steps, b, c.features), dtype=np.float32)
         storage = WeightStorage.AS_MODEL if mixed else WeightStorage.BF16
         with BatchRuntime((c, weights, mixed), b, storage, resident=resident) as rt:
+            if eager:
+                rt.set_eager()
             rt.device_run(events[:c.window])
             mean, per = rt.device_run(events[c.window:])
         p50 = nearest_rank(per, 0.5)
@@ -418,6 +423,11 @@ def main():
                     help='only the batched-streams measurement (B in 1, 16, 64, 256; --steps timed steps each)')
     ap.add_argument('--resident', action='store_true',
                     help='with --batched: only the resident rows (B in 1, 4, 16, 32)')
+    ap.add_argument('--eager', action='store_true',
+                    help='with --batched: only the bfloat16-weight phase-kernel rows, each step\'s kernels '
+                         'launched directly instead of the graph replay (for kernel traces)')
+    ap.add_argument('--streams', default='1,16,64,256',
+                    help='with --batched --eager: the batch sizes (comma-separated)')
     ap.add_argument('--copy-calibration', type=int, metavar='MIB', default=0,
                     help='only run 8 plain device copies of MIB MiB (reference kernel for HBM counters)')
     args = ap.parse_args()
@@ -431,6 +441,10 @@ def main():
     if args.batched and args.resident:
         print(json.dumps({'resident_bf16w': batched_streams(counts=(1, 4, 16, 32), steps=args.steps, resident=True)}),
               flush=True)
+        return
+    if args.batched and args.eager:
+        counts = tuple(int(b) for b in args.streams.split(','))
+        print(json.dumps({'bf16w': batched_streams(counts=counts, steps=args.steps, eager=True)}), flush=True)
         return
     if args.batched:
         print(json.dumps({'bf16w': batched_streams(steps=args.steps),

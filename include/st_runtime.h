@@ -255,6 +255,11 @@ int st_batch_snapshot(st_batch* batch, int32_t stream, uint64_t* position, float
  * when per_step_us is not NULL, each step's event-to-event duration. */
 int st_batch_device_run(st_batch* batch, const float* inputs, size_t count, double* us_per_step,
                         double* per_step_us);
+/* Phase-kernel batches: 1 launches each step's kernels directly instead of replaying the
+ * captured graph (so that a kernel trace sees plain launches; the results are the same), 0
+ * restores the replay. Resident batches already launch one kernel per step: for them the call
+ * changes nothing. No counterpart in the reference, which has no batched streams. */
+int st_batch_set_eager(st_batch* batch, int32_t eager);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* st_last_error(void);

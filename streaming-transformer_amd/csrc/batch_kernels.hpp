@@ -32,7 +32,8 @@ struct BatchArgs {
   uint32_t w_input, w_final_norm, w_score;
   LayerWeights layer[kMaxLayers];
   const float* rope_freq;          // [dim / 2]
-  void* keys;                      // [B][L][H][W][dh], FP32 (FP16 in mixed mode)
+  void* keys;                      // [L][B][H][W][dh], FP32 (FP16 in mixed mode): layer-major, so
+                                   // that one layer's attention reads one contiguous region
   void* values;
   float* hidden;                   // [B][L][d]
   unsigned long long* position;    // [B]
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
       } else {
         const int h = i / a.dim, d = i - h * a.dim;
         const int slot = (int)(pos % (unsigned long long)a.window);
-        const size_t ring = ((((size_t)b * a.layers + layer) * a.heads + h) * a.window + slot) * a.dim + d;
+        const size_t ring = ((((size_t)layer * a.streams + b) * a.heads + h) * a.window + slot) * a.dim + d;
         void* dst = sec == 1 ? a.keys : a.values;
         if constexpr (P == kMixed) {
           reinterpret_cast<uint16_t*>(dst)[ring] = float_to_half(va);
@@ -416,6 +417,101 @@ __device__ __forceinline__ float4 ring4(const void* ring, size_t i) {
   }
 }
 
+constexpr int kAttnThreads = 256;  // batch_attention's workgroup: four waves, 16 groups of 16 lanes
+constexpr int kAttnPasses = 4;     // passes of 16 rows per chunk of loads (dh <= 64)
+
+// batch_attention for dh <= 64: lane (group grp, r) holds elements 4r .. 4r + 3 of its rows,
+// one 16-byte load per row. The arithmetic is the general loop's, in the same order: per row a
+// dot product over the lane's four elements and a 16-lane sum; per group the V rows of slots
+// grp, grp + 16, ... accumulated in slot order.
+template <int P>
+__device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int h, int valid, size_t base,
+                                                  const float* q, float div, float* pr, float* wred,
+                                                  float4 (*vred)[17]) {
+  constexpr int kRows = 16 * kAttnPasses;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = tid & 15, grp = tid >> 4;
+  const int d = 4 * r;
+  const bool in = d < a.dim;
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float4 qv = in ? *reinterpret_cast<const float4*>(q + d) : z4;
+  // Slots past `valid` load slot valid - 1 and are dropped.
+  auto at = [&](int s) { return base + (size_t)(s < valid ? s : valid - 1) * a.dim + d; };
+  float mx = -INFINITY;
+  for (int c0 = 0; c0 < valid; c0 += kRows) {
+    float4 kv[kAttnPasses];
+#pragma unroll
+    for (int p = 0; p < kAttnPasses; p++) kv[p] = in ? ring4<P>(a.keys, at(c0 + 16 * p + grp)) : z4;
+#pragma unroll
+    for (int p = 0; p < kAttnPasses; p++) {
+      const int s = c0 + 16 * p + grp;
+      float dot = 0.f;
+      if (in) {
+        dot += qv.x * kv[p].x;
+        dot += qv.y * kv[p].y;
+        dot += qv.z * kv[p].z;
+        dot += qv.w * kv[p].w;
+      }
+      dot = group_sum(dot, 16);
+      if (s < valid) {
+        const float lg = dot / div;
+        if (r == 0) pr[s] = lg;
+        mx = fmaxf(mx, lg);
+      }
+    }
+  }
+  mx = wave_top(mx);
+  if (lane == 0) wred[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+  float sum = 0.f;
+  for (int s = tid; s < valid; s += kAttnThreads) {
+    const float e = expf(pr[s] - mx);
+    pr[s] = e;
+    sum += e;
+  }
+  sum = wave_total(sum);
+  __syncthreads();  // every wave has read wred (max) and written its probabilities
+  if (lane == 0) wred[wave] = sum;
+  __syncthreads();
+  sum = (wred[0] + wred[1]) + (wred[2] + wred[3]);
+  float4 o = z4;
+  for (int c0 = 0; c0 < valid; c0 += kRows) {
+    float4 vv[kAttnPasses];
+#pragma unroll
+    for (int p = 0; p < kAttnPasses; p++) vv[p] = in ? ring4<P>(a.values, at(c0 + 16 * p + grp)) : z4;
+#pragma unroll
+    for (int p = 0; p < kAttnPasses; p++) {
+      const int s = c0 + 16 * p + grp;
+      if (s < valid) {
+        const float pp = pr[s];
+        o.x += pp * vv[p].x;
+        o.y += pp * vv[p].y;
+        o.z += pp * vv[p].z;
+        o.w += pp * vv[p].w;
+      }
+    }
+  }
+  vred[grp][r] = o;
+  __syncthreads();
+  if (tid < 16 && 4 * tid < a.dim) {
+    float4 acc = vred[0][tid];
+    for (int k = 1; k < 16; k++) {
+      const float4 v = vred[k][tid];
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
+    }
+    const float o4[4] = {acc.x / sum, acc.y / sum, acc.z / sum, acc.w / sum};
+    const size_t oi = (size_t)b * a.width_p + h * a.dim + 4 * tid;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      if constexpr (P == kMixed) reinterpret_cast<uint16_t*>(a.attn)[oi + j] = float_to_half(o4[j]);
+      else a.attn[oi + j] = o4[j];
+    }
+  }
+}
+
 // Attention of one (stream, head) over the stream's valid ring slots [0, valid)
 // (src/cuda/Primitives.cuh:167-219): logits q.K/sqrt(dh), softmax, weighted V, cast. Slot order
 // does not change the result beyond summation order. Four waves; every load is a coalesced
@@ -425,8 +521,12 @@ __device__ __forceinline__ float4 ring4(const void* ring, size_t i) {
 //  - softmax: workgroup max and sum through LDS;
 //  - values: lane group (slot s mod 16) accumulates its slots' V rows, 4 elements per lane,
 //    and the 16 groups are summed in LDS in group order.
-// Needs dh a multiple of 4; dynamic LDS holds `window` floats of probabilities.
-constexpr int kAttnThreads = 256;
+// Needs dh a multiple of 4; dynamic LDS holds `window` floats of probabilities. For dh <= 64
+// (one 16-byte chunk per lane and row) the K and V rows are loaded in chunks of four passes
+// (64 slots), all of a chunk's loads issued before its arithmetic, in the same order of
+// operations. The rings are layer-major, so a layer's K and V are one contiguous region:
+// measured on Main at 256 streams, a layer's attention takes 23.1 us against 26.4 us in the
+// stream-major layout with the per-pass loop (5.8 against 5.1 TB/s).
 template <int P>
 __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs* __restrict__ ap, int layer) {
   const BatchArgs& a = *ap;
@@ -438,9 +538,13 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
   const int dim = a.dim, r = tid & 15, grp = tid >> 4;  // 16 groups of 16 lanes
   const unsigned long long t = a.position[b];
   const int valid = t + 1 < (unsigned long long)a.window ? (int)(t + 1) : a.window;
-  const size_t base = (((size_t)b * a.layers + layer) * a.heads + h) * (size_t)a.window * dim;
+  const size_t base = (((size_t)layer * a.streams + b) * a.heads + h) * (size_t)a.window * dim;
   const float* q = a.q + (size_t)b * a.width + h * dim;
   const float div = sqrtf((float)dim);
+  if (dim <= 64) {
+    attention_chunked<P>(a, b, h, valid, base, q, div, pr, wred, vred);
+    return;
+  }
   float mx = -INFINITY;
   // Rows past `valid` load row valid - 1 and are dropped, so the loop body has no branch
   // around its loads and several passes of loads stay in flight.
@@ -570,16 +674,19 @@ __global__ __launch_bounds__(64) void batch_final(const BatchArgs* __restrict__ 
 }
 
 // Zero the state of stream `stream` (every stream when negative): K/V rows, hidden, position.
-// `kv_words` is the size of one stream's K (or V) ring in 4-byte words.
-__global__ void batch_reset(const BatchArgs* __restrict__ ap, int stream, size_t kv_words) {
+// `block_words` is one (layer, stream) block of the K (or V) ring, [H][W][dh], in 4-byte words;
+// a stream's K/V is one such block in each layer (the rings are layer-major).
+__global__ void batch_reset(const BatchArgs* __restrict__ ap, int stream, size_t block_words) {
   const BatchArgs& a = *ap;
   const int b0 = stream < 0 ? 0 : stream, b1 = stream < 0 ? a.streams : stream + 1;
   const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x, step = (size_t)gridDim.x * blockDim.x;
   unsigned* k = reinterpret_cast<unsigned*>(a.keys);
   unsigned* v = reinterpret_cast<unsigned*>(a.values);
-  for (size_t i = (size_t)b0 * kv_words + tid; i < (size_t)b1 * kv_words; i += step) {
-    k[i] = 0u;
-    v[i] = 0u;
+  const size_t span = (size_t)(b1 - b0) * block_words;  // the streams' words in one layer
+  for (size_t i = tid; i < (size_t)a.layers * span; i += step) {
+    const size_t l = i / span, j = ((size_t)l * a.streams + b0) * block_words + i % span;
+    k[j] = 0u;
+    v[j] = 0u;
   }
   const size_t hper = (size_t)a.layers * a.width;
   for (size_t i = (size_t)b0 * hper + tid; i < (size_t)b1 * hper; i += step) a.hidden[i] = 0.f;

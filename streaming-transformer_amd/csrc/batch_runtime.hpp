@@ -14,6 +14,8 @@ class BatchBase {
   virtual void reset(int stream) = 0;
   virtual void snapshot(int stream, uint64_t* position, float* keys, float* values, float* hidden) = 0;
   virtual double device_run(const float* inputs, size_t count, double* per_step) = 0;
+  // Launch each step's kernels directly instead of replaying a captured graph (same results).
+  virtual void set_eager(bool) {}
 };
 
 class Batch : public BatchBase {
@@ -24,14 +26,20 @@ class Batch : public BatchBase {
   void reset(int stream) override;
   void snapshot(int stream, uint64_t* position, float* keys, float* values, float* hidden) override;
   double device_run(const float* inputs, size_t count, double* per_step) override;
+  void set_eager(bool eager) override { eager_ = eager; }
 
  private:
+  bool eager_ = false;  // launch the step's kernels directly (for kernel traces)
+  void replay() {
+    if (eager_) launch();
+    else HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
+  }
   template <int P> void launch_sequence();
   template <int P, int E, bool kNorm, int CT, int SW>
   void project(const void* X, int ld, uint32_t woff, int N, uint32_t norm, int layer, int max_tiles = kGroupTiles);
   int group_tiles(int cols, int max_tiles) const;
   bool wide_qkv_ = false, wide_gateup_ = false;  // two column tiles per workgroup
-  size_t kv_words_ = 0;                           // one stream's K (or V) ring in 4-byte words
+  size_t block_words_ = 0;  // one (layer, stream) block [H][W][dh] of the K (or V) ring, in 4-byte words
   void launch() {
     if (prec_ == kFp32) launch_sequence<kFp32>();
     else if (prec_ == kMixed) launch_sequence<kMixed>();
@@ -118,10 +126,10 @@ Batch::Batch(const st_config& config, bool mixed, const st_tensor* tensors, size
     HIP_CHECK(hipMemset(buf.ptr, 0, std::max<size_t>(floats * 4, 256)));
     return reinterpret_cast<float*>(buf.ptr);
   };
-  // K/V rings: FP32, or FP16 in mixed mode (kv_words_ 4-byte words per stream and ring).
-  kv_words_ = (size_t)c_.layers * c_.width * c_.window * (prec_ == kMixed ? 2 : 4) / 4;
-  a.keys = zeroed(keys_, (size_t)streams_ * kv_words_);
-  a.values = zeroed(values_, (size_t)streams_ * kv_words_);
+  // K/V rings [L][B][H][W][dh]: FP32, or FP16 in mixed mode.
+  block_words_ = (size_t)c_.width * c_.window * (prec_ == kMixed ? 2 : 4) / 4;
+  a.keys = zeroed(keys_, (size_t)c_.layers * streams_ * block_words_);
+  a.values = zeroed(values_, (size_t)c_.layers * streams_ * block_words_);
   a.hidden = zeroed(hidden_, (size_t)streams_ * c_.layers * c_.width);
   position_.alloc((size_t)streams_ * 8);
   HIP_CHECK(hipMemset(position_.ptr, 0, (size_t)streams_ * 8));
@@ -235,7 +243,7 @@ void Batch::step(const float* inputs, float* scores) {
   float* h = reinterpret_cast<float*>(host_in_.ptr);
   for (int b = 0; b < streams_; b++) std::memcpy(h + (size_t)b * fp, inputs + (size_t)b * c_.features, (size_t)c_.features * 4);
   HIP_CHECK(hipMemcpyAsync(args_.in, host_in_.ptr, (size_t)streams_p_ * fp * 4, hipMemcpyHostToDevice, stream_));
-  HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
+  replay();
   HIP_CHECK(hipMemcpyAsync(host_out_.ptr, args_.score, (size_t)streams_ * 4, hipMemcpyDeviceToHost, stream_));
   sync();
   std::memcpy(scores, host_out_.ptr, (size_t)streams_ * 4);
@@ -243,7 +251,7 @@ void Batch::step(const float* inputs, float* scores) {
 
 void Batch::reset(int stream) {
   if (stream < -1 || stream >= streams_) throw Error(ST_ERR_INVALID, "Stream index out of range");
-  hipLaunchKernelGGL(batch_reset, dim3(256), dim3(256), 0, stream_, dargs_, stream, kv_words_);
+  hipLaunchKernelGGL(batch_reset, dim3(256), dim3(256), 0, stream_, dargs_, stream, block_words_);
   HIP_CHECK(hipGetLastError());
   sync();
 }
@@ -254,15 +262,17 @@ void Batch::snapshot(int stream, uint64_t* position, float* keys, float* values,
   const size_t ring = (size_t)c_.layers * c_.width * c_.window;
   if (position)
     HIP_CHECK(hipMemcpy(position, args_.position + stream, 8, hipMemcpyDeviceToHost));
+  // The stream's block of each layer (layer-major rings) into [L][H][W][dh].
   auto download = [&](const void* base, float* dst) {
     if (!dst) return;
-    const char* src = reinterpret_cast<const char*>(base) + (size_t)stream * kv_words_ * 4;
+    const size_t block = block_words_ * 4, pitch = (size_t)streams_ * block;
+    const char* src = reinterpret_cast<const char*>(base) + (size_t)stream * block;
     if (prec_ == kMixed) {
       std::vector<uint16_t> h(ring);
-      HIP_CHECK(hipMemcpy(h.data(), src, ring * 2, hipMemcpyDeviceToHost));
+      HIP_CHECK(hipMemcpy2D(h.data(), block, src, pitch, block, c_.layers, hipMemcpyDeviceToHost));
       for (size_t i = 0; i < ring; i++) dst[i] = host_half_to_float(h[i]);
     } else {
-      HIP_CHECK(hipMemcpy(dst, src, ring * 4, hipMemcpyDeviceToHost));
+      HIP_CHECK(hipMemcpy2D(dst, block, src, pitch, block, c_.layers, hipMemcpyDeviceToHost));
     }
   };
   download(args_.keys, keys);
@@ -296,7 +306,7 @@ double Batch::device_run(const float* inputs, size_t count, double* per_step) {
   for (size_t i = 0; i < count; i++) {
     HIP_CHECK(hipMemcpyAsync(args_.in, reinterpret_cast<float*>(dev.ptr) + i * (size_t)streams_p_ * fp,
                              (size_t)streams_p_ * fp * 4, hipMemcpyDeviceToDevice, stream_));
-    HIP_CHECK(hipGraphLaunch(graph_exec_, stream_));
+    replay();
     HIP_CHECK(hipEventRecord(ev[i + 1], stream_));
   }
   sync();

@@ -1980,6 +1980,14 @@ int st_batch_device_run(st_batch* r, const float* inputs, size_t count, double* 
   });
 }
 
+int st_batch_set_eager(st_batch* r, int32_t eager) {
+  return guarded([&] {
+    if (!r) throw stamd::Error(ST_ERR_INVALID, "Null argument");
+    if (eager != 0 && eager != 1) throw stamd::Error(ST_ERR_INVALID, "eager must be 0 or 1");
+    r->impl->set_eager(eager != 0);
+  });
+}
+
 const char* st_last_error(void) { return stamd::g_last_error.c_str(); }
 
 }  // extern "C"

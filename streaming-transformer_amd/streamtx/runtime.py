@@ -120,7 +120,9 @@ def library(path: os.PathLike | None = None) -> ctypes.CDLL:
     lib.st_batch_reset.argtypes = [P, ctypes.c_int32]
     lib.st_batch_snapshot.argtypes = [P, ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64), F, F, F]
     lib.st_batch_device_run.argtypes = [P, F, ctypes.c_size_t, D, D]
-    for name in ('st_batch_create', 'st_batch_create_resident', 'st_batch_step', 'st_batch_reset', 'st_batch_snapshot', 'st_batch_device_run',
+    lib.st_batch_set_eager.argtypes = [P, ctypes.c_int32]
+    for name in ('st_batch_create', 'st_batch_create_resident', 'st_batch_step', 'st_batch_reset', 'st_batch_snapshot',
+                 'st_batch_device_run', 'st_batch_set_eager',
                  'st_runtime_create', 'st_runtime_step', 'st_runtime_reset', 'st_runtime_stop',
                  'st_runtime_snapshot', 'st_runtime_device_trace', 'st_runtime_device_trace_noalloc',
                  'st_runtime_device_run', 'st_runtime_phase_times',
@@ -439,3 +441,8 @@ class BatchRuntime:
         _check(library().st_batch_device_run(self._handle(), _fptr(x), x.shape[0], ctypes.byref(mean),
                                              per.ctypes.data_as(ctypes.POINTER(ctypes.c_double))))
         return float(mean.value), per
+
+    def set_eager(self, eager: bool = True) -> None:
+        """Launch each step's kernels directly instead of replaying the captured graph (the
+        phase-kernel path; the same results). For kernel traces."""
+        _check(library().st_batch_set_eager(self._handle(), 1 if eager else 0))

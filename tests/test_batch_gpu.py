@@ -7,13 +7,15 @@ Bars, through the C ABI:
   - a stream's results do not depend on the batch around it: stream b of a batch of B is
     bit-identical to a batch of 1 fed the same events (every output element of the MFMA
     tiles and the split-K reduction is a function of that stream's row only);
-  - per-stream reset touches only its stream; device_run equals stepping bit for bit.
+  - per-stream reset touches only its stream; device_run equals stepping bit for bit;
+  - eager launches (st_batch_set_eager) equal the graph replay bit for bit.
 """
 import numpy as np
 import pytest
 
 from oracle.pyoracle import Oracle
 from streamtx import BatchRuntime, ModelConfig, WeightStorage, numerical, round_bf16, synthetic_checkpoint
+from streamtx.runtime import _check, library
 
 pytestmark = pytest.mark.gpu
 
@@ -177,6 +179,30 @@ def test_reset_one_and_all_and_device_run_equals_stepping():
         np.testing.assert_array_equal(rt.step(events[-1]), stepped[-1])
 
 
+@pytest.mark.parametrize('weights,mixed,streams', [
+    (WeightStorage.BF16, False, 256),
+    (WeightStorage.AS_MODEL, True, 70),
+])
+def test_eager_launches_equal_the_graph_replay(weights, mixed, streams):
+    c = SHAPES['main']
+    w = synthetic_checkpoint(c, seed=16, mixed=mixed)
+    steps = c.window + 8
+    events = _events(c, 16, steps, streams)
+    runs = []
+    for eager in (False, True):
+        with batch((c, w, mixed), streams, weights) as rt:
+            rt.set_eager(eager)
+            scores = [rt.step(events[i]) for i in range(4)]
+            rt.device_run(events[4:steps - 1])
+            scores.append(rt.step(events[steps - 1]))
+            runs.append((np.stack(scores), [rt.snapshot(b) for b in (0, streams // 2, streams - 1)]))
+    np.testing.assert_array_equal(runs[0][0], runs[1][0])
+    for a, b in zip(runs[0][1], runs[1][1]):
+        assert a[0] == b[0] == steps
+        for x, y in zip(a[1:], b[1:]):
+            np.testing.assert_array_equal(x, y)
+
+
 def test_invalid_arguments_are_rejected():
     c = SHAPES['small']
     w = synthetic_checkpoint(c, seed=15)
@@ -195,3 +221,5 @@ def test_invalid_arguments_are_rejected():
             rt.snapshot(-1)
         with pytest.raises(ValueError):
             rt.step(np.zeros((3, c.features), dtype=np.float32))
+        with pytest.raises(RuntimeError, match='eager'):
+            _check(library().st_batch_set_eager(rt._handle(), 2))
