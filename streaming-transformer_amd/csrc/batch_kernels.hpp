@@ -418,31 +418,34 @@ __device__ __forceinline__ float4 ring4(const void* ring, size_t i) {
 }
 
 constexpr int kAttnThreads = 256;  // batch_attention's workgroup: four waves, 16 groups of 16 lanes
-constexpr int kAttnPasses = 4;     // passes of 16 rows per chunk of loads (dh <= 64)
 
 // batch_attention for dh <= 64: lane (group grp, r) holds elements 4r .. 4r + 3 of its rows,
-// one 16-byte load per row. The arithmetic is the general loop's, in the same order: per row a
-// dot product over the lane's four elements and a 16-lane sum; per group the V rows of slots
-// grp, grp + 16, ... accumulated in slot order.
-template <int P>
+// one 16-byte load per row, the loads of NP passes of 16 rows issued together; with kEarlyV the
+// first chunk's V loads are issued before the softmax reductions. The arithmetic is the general
+// loop's, in the same order: per row a dot product over the lane's four elements and a 16-lane
+// sum; per group the V rows of slots grp, grp + 16, ... accumulated in slot order.
+template <int P, int NP, bool kEarlyV>
 __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int h, int valid, size_t base,
                                                   const float* q, float div, float* pr, float* wred,
                                                   float4 (*vred)[17]) {
-  constexpr int kRows = 16 * kAttnPasses;
+  constexpr int kRows = 16 * NP;
+  const int dim = a.dim;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = tid & 15, grp = tid >> 4;
   const int d = 4 * r;
-  const bool in = d < a.dim;
+  const bool in = d < dim;
   const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
   const float4 qv = in ? *reinterpret_cast<const float4*>(q + d) : z4;
   // Slots past `valid` load slot valid - 1 and are dropped.
-  auto at = [&](int s) { return base + (size_t)(s < valid ? s : valid - 1) * a.dim + d; };
+  auto at = [&](int s) { return base + (size_t)(s < valid ? s : valid - 1) * dim + d; };
+  // V rows of a chunk; filled in place (an array filled through a lambda went to scratch).
+  float4 vv[NP];
   float mx = -INFINITY;
   for (int c0 = 0; c0 < valid; c0 += kRows) {
-    float4 kv[kAttnPasses];
+    float4 kv[NP];
 #pragma unroll
-    for (int p = 0; p < kAttnPasses; p++) kv[p] = in ? ring4<P>(a.keys, at(c0 + 16 * p + grp)) : z4;
+    for (int p = 0; p < NP; p++) kv[p] = in ? ring4<P>(a.keys, at(c0 + 16 * p + grp)) : z4;
 #pragma unroll
-    for (int p = 0; p < kAttnPasses; p++) {
+    for (int p = 0; p < NP; p++) {
       const int s = c0 + 16 * p + grp;
       float dot = 0.f;
       if (in) {
@@ -458,6 +461,10 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
         mx = fmaxf(mx, lg);
       }
     }
+  }
+  if constexpr (kEarlyV) {
+#pragma unroll
+    for (int p = 0; p < NP; p++) vv[p] = in ? ring4<P>(a.values, at(16 * p + grp)) : z4;
   }
   mx = wave_top(mx);
   if (lane == 0) wred[wave] = mx;
@@ -476,11 +483,12 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
   sum = (wred[0] + wred[1]) + (wred[2] + wred[3]);
   float4 o = z4;
   for (int c0 = 0; c0 < valid; c0 += kRows) {
-    float4 vv[kAttnPasses];
+    if (!kEarlyV || c0 > 0) {
 #pragma unroll
-    for (int p = 0; p < kAttnPasses; p++) vv[p] = in ? ring4<P>(a.values, at(c0 + 16 * p + grp)) : z4;
+      for (int p = 0; p < NP; p++) vv[p] = in ? ring4<P>(a.values, at(c0 + 16 * p + grp)) : z4;
+    }
 #pragma unroll
-    for (int p = 0; p < kAttnPasses; p++) {
+    for (int p = 0; p < NP; p++) {
       const int s = c0 + 16 * p + grp;
       if (s < valid) {
         const float pp = pr[s];
@@ -493,7 +501,7 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
   }
   vred[grp][r] = o;
   __syncthreads();
-  if (tid < 16 && 4 * tid < a.dim) {
+  if (tid < 16 && 4 * tid < dim) {
     float4 acc = vred[0][tid];
     for (int k = 1; k < 16; k++) {
       const float4 v = vred[k][tid];
@@ -503,7 +511,7 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
       acc.w += v.w;
     }
     const float o4[4] = {acc.x / sum, acc.y / sum, acc.z / sum, acc.w / sum};
-    const size_t oi = (size_t)b * a.width_p + h * a.dim + 4 * tid;
+    const size_t oi = (size_t)b * a.width_p + h * dim + 4 * tid;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       if constexpr (P == kMixed) reinterpret_cast<uint16_t*>(a.attn)[oi + j] = float_to_half(o4[j]);
@@ -521,13 +529,20 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
 //  - softmax: workgroup max and sum through LDS;
 //  - values: lane group (slot s mod 16) accumulates its slots' V rows, 4 elements per lane,
 //    and the 16 groups are summed in LDS in group order.
-// Needs dh a multiple of 4; dynamic LDS holds `window` floats of probabilities. For dh <= 64
-// (one 16-byte chunk per lane and row) the K and V rows are loaded in chunks of four passes
-// (64 slots), all of a chunk's loads issued before its arithmetic, in the same order of
-// operations. The rings are layer-major, so a layer's K and V are one contiguous region:
-// measured on Main at 256 streams, a layer's attention takes 23.1 us against 26.4 us in the
-// stream-major layout with the per-pass loop (5.8 against 5.1 TB/s).
-template <int P>
+// Needs dh a multiple of 4; dynamic LDS holds `window` floats of probabilities. The rings are
+// layer-major, so a layer's K and V are one contiguous region. kLoads picks the form of the
+// loops, on the host, by storage and batch size; every form computes the same values in the same
+// order, so a stream's bits do not depend on it:
+//  - kAttnPerPass: the general loop below, one pass of 16 rows after the other (any dh);
+//  - kAttnChunk4 / kAttnChunk8: dh <= 64, the loads of 4 or 8 passes issued together
+//    (attention_chunked), kAttnChunk4Early with the first V chunk loaded before the softmax.
+// Measured on Main (one layer, W = 128): with FP32 K/V at 256 streams 23.2 us against 26.2 us
+// for the per-pass loop in the former stream-major layout, at 64 streams 6.95 (4, early V)
+// against 8.8, at 16 streams 5.2 (8) against 7.4; with FP16 K/V the per-pass loop is faster up to
+// 64 streams (B = 1: 3.1 against 4.0 us; B = 64: 7.8 against 8.2) and four passes at 256
+// (16.4 against 17.2 us).
+enum AttnLoads : int { kAttnPerPass = 0, kAttnChunk4, kAttnChunk8, kAttnChunk4Early };
+template <int P, int kLoads>
 __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs* __restrict__ ap, int layer) {
   const BatchArgs& a = *ap;
   extern __shared__ float pr[];
@@ -541,8 +556,9 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
   const size_t base = (((size_t)layer * a.streams + b) * a.heads + h) * (size_t)a.window * dim;
   const float* q = a.q + (size_t)b * a.width + h * dim;
   const float div = sqrtf((float)dim);
-  if (dim <= 64) {
-    attention_chunked<P>(a, b, h, valid, base, q, div, pr, wred, vred);
+  if constexpr (kLoads != kAttnPerPass) {
+    constexpr int np = kLoads == kAttnChunk8 ? 8 : 4;
+    attention_chunked<P, np, kLoads == kAttnChunk4Early>(a, b, h, valid, base, q, div, pr, wred, vred);
     return;
   }
   float mx = -INFINITY;

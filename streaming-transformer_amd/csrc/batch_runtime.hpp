@@ -207,6 +207,11 @@ void Batch::launch_sequence() {
   const int d = c_.width, F = c_.ffn;
   const bool wide = streams_p_ >= 64, narrow = streams_p_ >= 128 && (c_.width / kBatchTile) % 2 == 0;
   const bool huge = P != kFp32 && streams_p_ >= 256;
+  // The attention loops' form (batch_attention): chunked loads for FP32 K/V with dh <= 64; for
+  // FP16 K/V only from 256 streams.
+  const int attn_loads = dim_ > 64 ? kAttnPerPass
+                         : P == kMixed ? (streams_p_ >= 256 ? kAttnChunk4 : kAttnPerPass)
+                         : streams_p_ <= 32 ? kAttnChunk8 : streams_p_ == 64 ? kAttnChunk4Early : kAttnChunk4;
   // Mixed mode casts each norm's output, so its norms run first into xn; the other modes fold
   // the norm into the projection (kNorm).
   constexpr bool kFold = P != kMixed;
@@ -222,8 +227,18 @@ void Batch::launch_sequence() {
     if (wide && wide_qkv_)
       project<P, kEpQkv, kFold, 2, 2>(nx, a.width_p, w.qkv, 3 * d, w.norm1, l, huge ? 1 : kGroupTiles);
     else project<P, kEpQkv, kFold, 1, 1>(nx, a.width_p, w.qkv, 3 * d, w.norm1, l);
-    hipLaunchKernelGGL(batch_attention<P>, dim3(streams_ * c_.heads), dim3(kAttnThreads), (size_t)c_.window * 4,
-                       stream_, dargs_, l);
+    {
+      const dim3 grid(streams_ * c_.heads), block(kAttnThreads);
+      const size_t lds = (size_t)c_.window * 4;
+      if (attn_loads == kAttnChunk4)
+        hipLaunchKernelGGL((batch_attention<P, kAttnChunk4>), grid, block, lds, stream_, dargs_, l);
+      else if (attn_loads == kAttnChunk8)
+        hipLaunchKernelGGL((batch_attention<P, kAttnChunk8>), grid, block, lds, stream_, dargs_, l);
+      else if (attn_loads == kAttnChunk4Early)
+        hipLaunchKernelGGL((batch_attention<P, kAttnChunk4Early>), grid, block, lds, stream_, dargs_, l);
+      else
+        hipLaunchKernelGGL((batch_attention<P, kAttnPerPass>), grid, block, lds, stream_, dargs_, l);
+    }
     if (narrow) project<P, kEpOut, false, 2, 1>(a.attn, a.width_p, w.out, d, 0u, l);
     else project<P, kEpOut, false, 1, 1>(a.attn, a.width_p, w.out, d, 0u, l);
     norm(w.norm2);
