@@ -93,7 +93,10 @@ def test_bf16_weights_match_oracle_on_rounded_weights():
 @pytest.mark.parametrize('weight_dtype,mixed,streams,steps', [
     (WeightStorage.AS_MODEL, False, 40, 70), (WeightStorage.BF16, False, 40, 70), (WeightStorage.AS_MODEL, True, 40, 70),
     # 130 streams: the large-batch workgroup shapes of every projection
-    (WeightStorage.BF16, False, 130, 20), (WeightStorage.AS_MODEL, True, 130, 20)])
+    (WeightStorage.BF16, False, 130, 20), (WeightStorage.AS_MODEL, True, 130, 20),
+    # 256 streams: mixed mode's attention switches to chunked loads (against the per-pass loop
+    # of a batch of one), past the window
+    (WeightStorage.AS_MODEL, True, 256, 70)])
 def test_stream_independent_of_batch(weight_dtype, mixed, streams, steps):
     c = SHAPES['small']
     w = synthetic_checkpoint(c, seed=13, mixed=mixed)
