@@ -28,6 +28,8 @@ SHAPES = {
     'ref-main': ModelConfig(2, 128, 4, 256, 256, 32),
     # head dim 48
     'dh48': ModelConfig(2, 96, 2, 192, 40, 96),
+    # head dim 128: attention's general per-pass loop (two 64-element passes per row)
+    'dh128': ModelConfig(2, 256, 2, 512, 48, 256),
 }
 
 
@@ -52,6 +54,7 @@ def _check_state(state, oracle_state):
     ('small', 19, 80, {7: 50, 18: 3}),
     ('ref-main', 17, 270, {0: 100}),
     ('dh48', 3, 60, {1: 41}),
+    ('dh128', 5, 60, {2: 30}),
     ('main', 16, 24, {5: 11}),
 ])
 def test_every_stream_matches_oracle(name, streams, steps, resets):
