@@ -107,12 +107,14 @@ def batched_streams(counts=(1, 16, 64, 256), steps=64, mode='bf16w', resident=Fa
     return out
 
 
-def torch_baseline(c: ModelConfig, weights, events, fill: int, steps: int = 128):
+def torch_baseline(c: ModelConfig, weights, events, fill: int, steps: int = 128, inductor: bool = False):
     """The same single-stream step written with PyTorch-ROCm operators in FP32 (the
     reference's bench/torch_bench.py comparison): eager, and captured once in a hipGraph with
     the position held on the device (ring slot, valid-window mask and RoPE angles computed from
     it). Returns p50 microseconds per step for both and the largest score difference from the
-    HIP runtime on the same events (a sanity check, not a parity bar)."""
+    HIP runtime on the same events (a sanity check, not a parity bar). With `inductor`, only
+    the reference's third variant instead: the step compiled by torch.compile (Inductor,
+    fullgraph), p50 per step, compile time and the largest score difference from eager."""
     import torch
 
     dev = torch.device('cuda')
@@ -175,6 +177,28 @@ def torch_baseline(c: ModelConfig, weights, events, fill: int, steps: int = 128)
             event.copy_(torch.from_numpy(events[i]).to(dev))
             step()
         state = (keys.clone(), values.clone(), pos.clone())  # the filled window
+        if inductor:
+            eager_scores = []
+            for i in range(8):
+                event.copy_(torch.from_numpy(events[fill + i]).to(dev))
+                step()
+                eager_scores.append(float(score))
+            compiled = torch.compile(step, fullgraph=True, backend='inductor')
+            keys.copy_(state[0]), values.copy_(state[1]), pos.copy_(state[2])
+            t0 = time.perf_counter()
+            event.copy_(torch.from_numpy(events[fill]).to(dev))
+            compiled()
+            torch.cuda.synchronize()
+            compile_s = time.perf_counter() - t0
+            diff = abs(float(score) - eager_scores[0])
+            for i in range(1, 8):
+                event.copy_(torch.from_numpy(events[fill + i]).to(dev))
+                compiled()
+                diff = max(diff, abs(float(score) - eager_scores[i]))
+            keys.copy_(state[0]), values.copy_(state[1]), pos.copy_(state[2])
+            per = timed(compiled, steps)
+            return {'inductor_p50_us': round(float(np.median(per)), 1), 'inductor_compile_s': round(compile_s, 1),
+                    'inductor_vs_eager_max_abs': diff, 'torch': torch.__version__}
         eager = timed(step, steps)
         eager_scores = []
         # Graph capture of the same step on a side stream, then replays checked against eager.
@@ -419,6 +443,8 @@ def main():
     ap.add_argument('--quick', action='store_true', help='skip the secondary measurements')
     ap.add_argument('--torch-baseline', action='store_true',
                     help='only the PyTorch comparison (FP32, eager and captured); bench.py runs it as a child')
+    ap.add_argument('--inductor', action='store_true',
+                    help='with --torch-baseline: the torch.compile (Inductor) variant instead')
     ap.add_argument('--batched', action='store_true',
                     help='only the batched-streams measurement (B in 1, 16, 64, 256; --steps timed steps each)')
     ap.add_argument('--resident', action='store_true',
@@ -436,7 +462,7 @@ def main():
         weights = synthetic_checkpoint(c, seed=seed)
         fill = c.window - 1 + args.warmup
         events = np.random.default_rng([seed, 1]).standard_normal((fill + 128, c.features), dtype=np.float32)
-        print(json.dumps(torch_baseline(c, weights, events, fill)), flush=True)
+        print(json.dumps(torch_baseline(c, weights, events, fill, inductor=args.inductor)), flush=True)
         return
     if args.batched and args.resident:
         print(json.dumps({'resident_bf16w': batched_streams(counts=(1, 4, 16, 32), steps=args.steps, resident=True)}),
@@ -560,13 +586,19 @@ def main():
         import subprocess
         cmd = [sys.executable, str(Path(__file__).resolve()), '--torch-baseline', '--config', args.config,
                '--warmup', str(args.warmup)]
-        try:
-            proc = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
-            lines = [ln for ln in proc.stdout.splitlines() if ln.startswith('{')]
-            extra['torch_baseline'] = json.loads(lines[-1]) if proc.returncode == 0 and lines else \
-                {'error': (proc.stderr or proc.stdout)[-300:]}
-        except subprocess.TimeoutExpired:
-            extra['torch_baseline'] = {'error': 'timeout'}
+        def child(extra_args, timeout):
+            try:
+                proc = subprocess.run(cmd + extra_args, capture_output=True, text=True, timeout=timeout)
+                lines = [ln for ln in proc.stdout.splitlines() if ln.startswith('{')]
+                return json.loads(lines[-1]) if proc.returncode == 0 and lines else \
+                    {'error': (proc.stderr or proc.stdout)[-300:]}
+            except subprocess.TimeoutExpired:
+                return {'error': 'timeout'}
+        extra['torch_baseline'] = child([], 300)
+        # The reference's third variant, torch.compile (Inductor), in a child of its own so that a
+        # compiler failure leaves the other two figures.
+        inductor = child(['--inductor'], 300)
+        extra['torch_baseline'].update(inductor if 'error' not in inductor else {'inductor_error': inductor['error']})
     if not args.quick and args.config == 'large' and args.precision == 'fp32':
         # The same Large workload in the other storage modes: mixed (FP16 weights and K/V, the
         # reference's cast points) and bfloat16 weights with FP32 K/V.
