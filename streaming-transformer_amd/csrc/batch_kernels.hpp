@@ -37,16 +37,60 @@ struct BatchArgs {
   void* values;
   float* hidden;                   // [B][L][d]
   unsigned long long* position;    // [B]
-  float* in;                       // [Bp][features_p] events
-  float* x;                        // [Bp][width_p] residual stream
-  float* xn;                       // [Bp][width_p] normalized x (mixed mode, FP16)
-  float* attn;                     // [Bp][width_p] attention output (FP16 in mixed mode)
-  float* act;                      // [Bp][ffn_p] SwiGLU output (FP16 in mixed mode)
+  // Activations, Bp rows of the padded lengths, in the tiled layouts (act_index, half_index):
+  float* in;                       // events (features_p)
+  float* x;                        // residual stream (width_p)
+  float* xn;                       // normalized x (mixed mode, FP16; width_p)
+  float* attn;                     // attention output (FP16 in mixed mode; width_p)
+  float* act;                      // SwiGLU output (FP16 in mixed mode; ffn_p)
   float* q;                        // [Bp][width] rotated queries
   float* score;                    // [B]
 };
 
 constexpr int kSlices = 8;       // K-slices of a projection, K / 8 columns each
+
+// Loads from the weight arena through the global address space. The arena's base arrives in
+// the arguments block as a generic pointer, and a load through a generic (flat) pointer also
+// counts on the LDS counter, so the compiler would wait for every outstanding load, the
+// prefetched ones included, before a block's first MFMA.
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 gload16(const void* p) {
+  return __builtin_bit_cast(uint4, *(const __attribute__((address_space(1))) u32x4_t*)p);
+}
+__device__ __forceinline__ float4 gload16f(const void* p) {
+  return __builtin_bit_cast(float4, *(const __attribute__((address_space(1))) u32x4_t*)p);
+}
+__device__ __forceinline__ uint2 gload8(const void* p) {
+  return __builtin_bit_cast(uint2, *(const __attribute__((address_space(1))) u32x2_t*)p);
+}
+
+// Activation layouts. The projections' operands (in, x, xn, attn, act) are stored the way the
+// weights are (the tiled arena): 16-row tiles of streams, then blocks of KB columns, then the
+// 64 lanes of the MFMA operand (stream b mod 16 + 16 x column group), so that a wave loads a
+// block as contiguous 16-byte runs in lane order. `cols` is the buffer's padded row length
+// (a multiple of 32).
+//  - FP32 buffers for the FP32 MFMA (FP32 storage; mixed mode's x and events): KB = 16, four
+//    floats per lane.
+//  - FP32 buffers for the bfloat16 MFMA (bfloat16 weights): KB = 32, eight floats per lane,
+//    stored as two planes of four (the lane's low and high halves), each plane 64 x 16 bytes.
+//  - FP16 buffers (mixed mode's xn, attn, act): KB = 32, eight halves per lane.
+// Four consecutive columns from a multiple of 4 are consecutive in every layout.
+template <int P>
+__host__ __device__ __forceinline__ size_t act_index(int b, int n, int cols) {
+  if constexpr (P == kBf16w) {
+    const int kk = n & 31;
+    return ((((size_t)(b >> 4) * (cols >> 5) + (n >> 5)) * 2 + ((kk >> 2) & 1)) * 64 + (b & 15) + 16 * (kk >> 3)) * 4 +
+           (kk & 3);
+  } else {
+    const int kk = n & 15;
+    return (((size_t)(b >> 4) * (cols >> 4) + (n >> 4)) * 64 + (b & 15) + 16 * (kk >> 2)) * 4 + (kk & 3);
+  }
+}
+__host__ __device__ __forceinline__ size_t half_index(int b, int n, int cols) {
+  const int kk = n & 31;
+  return (((size_t)(b >> 4) * (cols >> 5) + (n >> 5)) * 64 + (b & 15) + 16 * (kk >> 3)) * 8 + (kk & 7);
+}
 constexpr int kGroupTiles = 4;   // most batch tiles (16 streams each) per projection workgroup
 
 enum BatchEpilogue : int { kEpInput = 0, kEpQkv, kEpOut, kEpGateUp, kEpDown };
@@ -75,6 +119,61 @@ __device__ __forceinline__ void split3(const float (&x)[8], unsigned (&ph)[4], u
   }
 }
 
+// The K loop of one wave over its SW slices, from slice `first`, in blocks of KB columns.
+// SW = 1: a ring of R fragments, unrolled so that no fragment is copied (a copy would wait for
+// its loads): block j + R is loaded into the fragment of block j as soon as block j's MFMAs are
+// issued, so R blocks are in flight while one computes. R = 4 for workgroups of at most two
+// tiles when the slice holds a multiple of 4 blocks (it always holds an even number), else 2.
+// Two kinds of empty asm statement hold the schedule: one after each prefetch (the compiler
+// would otherwise see that the loads only feed the next round and move them next to their
+// use), and `pin`, which passes a fragment's registers through an asm right before its MFMAs
+// (the compiler would otherwise hoist the operand arithmetic of every fragment to the top of
+// the round, which waits for all loads in flight). Either way every block would wait a full
+// memory round trip. SW = 2: each step loads one block of each of the two slices, then runs
+// both. Every form issues a slice's MFMAs in block order.
+template <int R, int KB, typename Frag, typename Load, typename Pin, typename Mma>
+__device__ __forceinline__ void k_ring(int k0, int nb, Load& load, Pin& pin, Mma& mma) {
+  Frag f[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) load(k0 + r * KB, f[r]);
+  asm volatile("" ::: "memory");
+  int j = 0;
+  for (; j + R < nb; j += R) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      pin(f[r]);
+      mma(0, f[r]);
+      load(k0 + (j + R + r) * KB, f[r]);
+      asm volatile("" ::: "memory");
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    pin(f[r]);
+    mma(0, f[r]);
+  }
+}
+
+__device__ __forceinline__ void pin4(uint4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
+__device__ __forceinline__ void pin4(float4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
+
+template <int SW, int KB, bool kSmall, typename Frag, typename Load, typename Pin, typename Mma>
+__device__ __forceinline__ void k_loop(int first, int slice, Load&& load, Pin&& pin, Mma&& mma) {
+  if constexpr (SW == 1) {
+    const int k0 = first * slice, nb = slice / KB;
+    if (kSmall && nb % 4 == 0) k_ring<4, KB, Frag>(k0, nb, load, pin, mma);
+    else k_ring<2, KB, Frag>(k0, nb, load, pin, mma);
+  } else {
+    for (int kk = 0; kk < slice; kk += KB) {
+      Frag f[SW];
+#pragma unroll
+      for (int i = 0; i < SW; i++) load((first + i) * slice + kk, f[i]);
+#pragma unroll
+      for (int i = 0; i < SW; i++) mma(i, f[i]);
+    }
+  }
+}
+
 // One projection Y = X . W^T over the batch, with its phase's epilogue. Workgroup: CT column
 // tiles of 16 outputs and NT batch tiles of 16 streams. K is cut into 8 slices; each wave
 // accumulates SW of them (8 / SW waves) for every tile pair with MFMA, reusing each X
@@ -82,7 +181,9 @@ __device__ __forceinline__ void split3(const float (&x)[8], unsigned (&ph)[4], u
 // partials are added in one fixed pairwise tree, ((s0 + s1) + (s2 + s3)) + ((s4 + s5) +
 // (s6 + s7)), whatever NT, CT and SW are, so a stream's outputs depend only on its own row
 // and are bit-identical for every batch size. The padded batch is a multiple of NT tiles, so
-// the loops have no branches.
+// the loops have no branches. X and W are in the tiled operand layout (act_index and the tiled
+// arena): one 16 x KB block of either is 64 lanes' contiguous 16-byte pieces in lane order.
+// X is the padded buffer of K columns; W the N x K matrix at arena offset `woff`.
 // FP32 weights: v_mfma_f32_16x16x4_f32, k block of 16; lane l supplies A[l % 16][l / 16] and
 // B[l / 16][l % 16], register r of lane l holds D[4 (l / 16) + r][l % 16]; the four MFMA
 // steps use k = kb + 4 (l / 16) + c for step c, the same index for A and B.
@@ -96,8 +197,8 @@ __device__ __forceinline__ void split3(const float (&x)[8], unsigned (&ph)[4], u
 // 1 / sqrt(sum / d + eps).
 template <int P, int E, bool kNorm, int NT, int CT, int SW>
 __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs* __restrict__ ap,
-                                                               const void* __restrict__ X, int ldx, uint32_t woff,
-                                                               int ldw, int N, int K, uint32_t w_norm, int layer) {
+                                                               const void* __restrict__ X, uint32_t woff, int N,
+                                                               int K, uint32_t w_norm, int layer) {
   constexpr int kWaves = kSlices / SW;
   const BatchArgs& a = *ap;
   __shared__ float red[kWaves][NT][CT][16][17];
@@ -106,7 +207,8 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
   const int n0 = blockIdx.x * kBatchTile * CT;
   const int t0 = blockIdx.y * NT;
   const int r16 = lane & 15, g = lane >> 4;
-  const int slice = K / kSlices;
+  const int slice = K / kSlices, width = a.width;
+  const int first = wave * SW;  // the wave's first slice
   f4v acc[SW][NT][CT];
   float ss[SW][NT];
 #pragma unroll
@@ -121,8 +223,10 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
   if constexpr (P == kFp32 || (P == kMixed && E == kEpInput)) {
     // FP32 MFMA. Mixed mode takes this path for the input projection only: its operand is
     // the raw FP32 event, and its FP16 weights widen exactly.
-    const float* xr = reinterpret_cast<const float*>(X) + (size_t)(t0 * kBatchTile + r16) * ldx + 4 * g;
-    const char* wr = a.weights + woff + ((size_t)(n0 + r16) * ldw + 4 * g) * (P == kFp32 ? 4 : 2);
+    // Tiled operands: block (tile, k / 16) holds 64 lanes x 4 values.
+    const int nkb = K / 16;
+    const float* xr = reinterpret_cast<const float*>(X) + ((size_t)t0 * nkb * 64 + lane) * 4;
+    const char* wr = a.weights + woff + ((size_t)(n0 / kBatchTile) * nkb * 64 + lane) * 4 * (P == kFp32 ? 4 : 2);
     const float* gr = reinterpret_cast<const float*>(a.weights + w_norm) + 4 * g;
     struct Frag {
       float4 w[CT], gn, x[NT];
@@ -130,11 +234,11 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
     auto load = [&](int k, Frag& f) {
 #pragma unroll
       for (int c = 0; c < CT; c++) {
+        const size_t blk = ((size_t)c * nkb + k / 16) * 256;
         if constexpr (P == kFp32) {
-          f.w[c] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(wr) + (size_t)c * kBatchTile * ldw + k);
+          f.w[c] = gload16f(reinterpret_cast<const float*>(wr) + blk);
         } else {
-          const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(wr) +
-                                                          (size_t)c * kBatchTile * ldw + k);
+          const uint2 h = gload8(reinterpret_cast<const uint16_t*>(wr) + blk);
           f.w[c] = make_float4(half_to_float((unsigned short)(h.x & 0xffffu)), half_to_float((unsigned short)(h.x >> 16)),
                                half_to_float((unsigned short)(h.y & 0xffffu)), half_to_float((unsigned short)(h.y >> 16)));
         }
@@ -142,9 +246,9 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
       // The norm vector holds `width` values (a multiple of 16): a group of 4 is all in or out.
       f.gn = make_float4(0.f, 0.f, 0.f, 0.f);
       if constexpr (kNorm)
-        if (k + 4 * g < a.width) f.gn = *reinterpret_cast<const float4*>(gr + k);
+        if (k + 4 * g < width) f.gn = gload16f(gr + k);
 #pragma unroll
-      for (int t = 0; t < NT; t++) f.x[t] = *reinterpret_cast<const float4*>(xr + (size_t)t * kBatchTile * ldx + k);
+      for (int t = 0; t < NT; t++) f.x[t] = *reinterpret_cast<const float4*>(xr + ((size_t)t * nkb + k / 16) * 256);
     };
     auto mma = [&](int i, const Frag& f) {
 #pragma unroll
@@ -170,29 +274,20 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
         }
       }
     };
-    if constexpr (SW == 1) {
-      // Issue the next block's loads before this block's MFMAs (the last block reloads itself).
-      const int k0 = wave * slice;
-      Frag cur;
-      load(k0, cur);
-      for (int kk = 0; kk < slice; kk += 16) {
-        Frag nxt;
-        load(k0 + (kk + 16 < slice ? kk + 16 : kk), nxt);
-        mma(0, cur);
-        cur = nxt;
-      }
-    } else {
-      for (int kk = 0; kk < slice; kk += 16) {
-        Frag f[SW];
+    auto pin = [&](Frag& f) {
 #pragma unroll
-        for (int i = 0; i < SW; i++) load((wave * SW + i) * slice + kk, f[i]);
+      for (int c = 0; c < CT; c++) pin4(f.w[c]);
 #pragma unroll
-        for (int i = 0; i < SW; i++) mma(i, f[i]);
-      }
-    }
+      for (int t = 0; t < NT; t++) pin4(f.x[t]);
+      if constexpr (kNorm) pin4(f.gn);
+    };
+    k_loop<SW, 16, NT * CT <= 2, Frag>(first, slice, load, pin, mma);
   } else if constexpr (P == kBf16w) {
-    const float* xr = reinterpret_cast<const float*>(X) + (size_t)(t0 * kBatchTile + r16) * ldx + 8 * g;
-    const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.weights + woff) + (size_t)(n0 + r16) * ldw + 8 * g;
+    // Tiled operands: weight block (tile, k / 32) holds 64 lanes x 8 values, activation block
+    // two planes of 64 lanes x 4 floats.
+    const int nkb = K / 32;
+    const float* xr = reinterpret_cast<const float*>(X) + ((size_t)t0 * nkb * 128 + lane) * 4;
+    const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.weights + woff) + ((size_t)(n0 / kBatchTile) * nkb * 64 + lane) * 8;
     const uint16_t* gr = reinterpret_cast<const uint16_t*>(a.weights + w_norm) + 8 * g;
     struct Frag {
       uint4 w[CT], gn;
@@ -200,15 +295,15 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
     };
     auto load = [&](int k, Frag& f) {
 #pragma unroll
-      for (int c = 0; c < CT; c++) f.w[c] = *reinterpret_cast<const uint4*>(wr + (size_t)c * kBatchTile * ldw + k);
+      for (int c = 0; c < CT; c++) f.w[c] = gload16(wr + ((size_t)c * nkb + k / 32) * 512);
       f.gn = make_uint4(0u, 0u, 0u, 0u);
       if constexpr (kNorm)
-        if (k + 8 * g < a.width) f.gn = *reinterpret_cast<const uint4*>(gr + k);
+        if (k + 8 * g < width) f.gn = gload16(gr + k);
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        const float* p = xr + (size_t)t * kBatchTile * ldx + k;
+        const float* p = xr + ((size_t)t * nkb + k / 32) * 512;
         f.xlo[t] = *reinterpret_cast<const float4*>(p);
-        f.xhi[t] = *reinterpret_cast<const float4*>(p + 4);
+        f.xhi[t] = *reinterpret_cast<const float4*>(p + 256);
       }
     };
     auto mma = [&](int i, const Frag& f) {
@@ -245,39 +340,33 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
         }
       }
     };
-    if constexpr (SW == 1) {
-      const int k0 = wave * slice;
-      Frag cur;
-      load(k0, cur);
-      for (int kk = 0; kk < slice; kk += 32) {
-        Frag nxt;
-        load(k0 + (kk + 32 < slice ? kk + 32 : kk), nxt);
-        mma(0, cur);
-        cur = nxt;
-      }
-    } else {
-      for (int kk = 0; kk < slice; kk += 32) {
-        Frag f[SW];
+    auto pin = [&](Frag& f) {
 #pragma unroll
-        for (int i = 0; i < SW; i++) load((wave * SW + i) * slice + kk, f[i]);
+      for (int c = 0; c < CT; c++) pin4(f.w[c]);
 #pragma unroll
-        for (int i = 0; i < SW; i++) mma(i, f[i]);
+      for (int t = 0; t < NT; t++) {
+        pin4(f.xlo[t]);
+        pin4(f.xhi[t]);
       }
-    }
+      if constexpr (kNorm) pin4(f.gn);
+    };
+    k_loop<SW, 32, NT * CT <= 2, Frag>(first, slice, load, pin, mma);
   } else {
     // Mixed mode: the operand is an FP16 buffer (its values are cast points) and the weights
     // are FP16; one v_mfma_f32_16x16x32_f16 per 32-k block, lane (r16, g) holding
     // k = kb + 8 g .. + 7 of both, 16 bytes each.
-    const uint16_t* xr = reinterpret_cast<const uint16_t*>(X) + (size_t)(t0 * kBatchTile + r16) * ldx + 8 * g;
-    const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.weights + woff) + (size_t)(n0 + r16) * ldw + 8 * g;
+    // Tiled operands: block (tile, k / 32) holds 64 lanes x 8 values.
+    const int nkb = K / 32;
+    const uint16_t* xr = reinterpret_cast<const uint16_t*>(X) + ((size_t)t0 * nkb * 64 + lane) * 8;
+    const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.weights + woff) + ((size_t)(n0 / kBatchTile) * nkb * 64 + lane) * 8;
     struct Frag {
       uint4 w[CT], x[NT];
     };
     auto load = [&](int k, Frag& f) {
 #pragma unroll
-      for (int c = 0; c < CT; c++) f.w[c] = *reinterpret_cast<const uint4*>(wr + (size_t)c * kBatchTile * ldw + k);
+      for (int c = 0; c < CT; c++) f.w[c] = gload16(wr + ((size_t)c * nkb + k / 32) * 512);
 #pragma unroll
-      for (int t = 0; t < NT; t++) f.x[t] = *reinterpret_cast<const uint4*>(xr + (size_t)t * kBatchTile * ldx + k);
+      for (int t = 0; t < NT; t++) f.x[t] = *reinterpret_cast<const uint4*>(xr + ((size_t)t * nkb + k / 32) * 512);
     };
     auto mma = [&](int i, const Frag& f) {
 #pragma unroll
@@ -287,25 +376,13 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
           acc[i][t][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, f.x[t]),
                                                                 __builtin_bit_cast(f16x8, f.w[c]), acc[i][t][c], 0, 0, 0);
     };
-    if constexpr (SW == 1) {
-      const int k0 = wave * slice;
-      Frag cur;
-      load(k0, cur);
-      for (int kk = 0; kk < slice; kk += 32) {
-        Frag nxt;
-        load(k0 + (kk + 32 < slice ? kk + 32 : kk), nxt);
-        mma(0, cur);
-        cur = nxt;
-      }
-    } else {
-      for (int kk = 0; kk < slice; kk += 32) {
-        Frag f[SW];
+    auto pin = [&](Frag& f) {
 #pragma unroll
-        for (int i = 0; i < SW; i++) load((wave * SW + i) * slice + kk, f[i]);
+      for (int c = 0; c < CT; c++) pin4(f.w[c]);
 #pragma unroll
-        for (int i = 0; i < SW; i++) mma(i, f[i]);
-      }
-    }
+      for (int t = 0; t < NT; t++) pin4(f.x[t]);
+    };
+    k_loop<SW, 32, NT * CT <= 2, Frag>(first, slice, load, pin, mma);
   }
   // A wave holding two slices adds them here: the first level of the tree.
 #pragma unroll
@@ -354,9 +431,9 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
     s0 = cast<P>(s0);
     s1 = cast<P>(s1);
     const int n = n0 + cc;
-    float* xb = a.x + (size_t)b * a.width_p;
+    float* xp = a.x + act_index<P>(b, n, a.width_p);  // x[b][n]
     if constexpr (E == kEpInput) {
-      xb[n] = s0;
+      *xp = s0;
     } else if constexpr (E == kEpQkv) {
       // src/cuda/Primitives.cuh:148-166: RoPE on adjacent pairs of q and k, then the ring write.
       const int sec = (n >= a.width) + (n >= 2 * a.width);
@@ -392,14 +469,14 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
         }
       }
     } else if constexpr (E == kEpOut) {
-      xb[n] = cast<P>(xb[n] + s0);
+      *xp = cast<P>(*xp + s0);
     } else if constexpr (E == kEpGateUp) {
       const float v = cast<P>((s0 / (1.0f + expf(-s0))) * s1);
-      if constexpr (P == kMixed) reinterpret_cast<uint16_t*>(a.act)[(size_t)b * a.ffn_p + (n >> 1)] = float_to_half(v);
-      else a.act[(size_t)b * a.ffn_p + (n >> 1)] = v;
+      if constexpr (P == kMixed) reinterpret_cast<uint16_t*>(a.act)[half_index(b, n >> 1, a.ffn_p)] = float_to_half(v);
+      else a.act[act_index<P>(b, n >> 1, a.ffn_p)] = v;
     } else {
-      const float v = cast<P>(xb[n] + s0);
-      xb[n] = v;
+      const float v = cast<P>(*xp + s0);
+      *xp = v;
       a.hidden[((size_t)b * a.layers + layer) * a.width + n] = v;
     }
   }
@@ -511,7 +588,9 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
       acc.w += v.w;
     }
     const float o4[4] = {acc.x / sum, acc.y / sum, acc.z / sum, acc.w / sum};
-    const size_t oi = (size_t)b * a.width_p + h * dim + 4 * tid;
+    // attn[b][h dh + 4 tid + j]: four consecutive elements in the tiled layouts too.
+    const int n = h * dim + 4 * tid;
+    const size_t oi = P == kMixed ? half_index(b, n, a.width_p) : act_index<P>(b, n, a.width_p);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       if constexpr (P == kMixed) reinterpret_cast<uint16_t*>(a.attn)[oi + j] = float_to_half(o4[j]);
@@ -625,7 +704,8 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
         acc.w += v.w;
       }
       const float o4[4] = {acc.x / sum, acc.y / sum, acc.z / sum, acc.w / sum};
-      const size_t oi = (size_t)b * a.width_p + h * dim + d0 + 4 * tid;
+      const int n = h * dim + d0 + 4 * tid;
+      const size_t oi = P == kMixed ? half_index(b, n, a.width_p) : act_index<P>(b, n, a.width_p);
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         if constexpr (P == kMixed) reinterpret_cast<uint16_t*>(a.attn)[oi + j] = float_to_half(o4[j]);
@@ -651,20 +731,21 @@ __global__ __launch_bounds__(256) void batch_norm_mixed(const BatchArgs* __restr
   const BatchArgs& a = *ap;
   __shared__ float red[4];
   const int b = blockIdx.x;
-  const float* xb = a.x + (size_t)b * a.width_p;
-  uint16_t* out = reinterpret_cast<uint16_t*>(a.xn) + (size_t)b * a.width_p;
+  const float* x = a.x;
+  uint16_t* out = reinterpret_cast<uint16_t*>(a.xn);
+  auto xb = [&](int i) { return x[act_index<kMixed>(b, i, a.width_p)]; };
   if (b >= a.streams) {
-    for (int i = threadIdx.x; i < a.width_p; i += blockDim.x) out[i] = 0;
+    for (int i = threadIdx.x; i < a.width_p; i += blockDim.x) out[half_index(b, i, a.width_p)] = 0;
     return;
   }
   float s = 0.f;
-  for (int i = threadIdx.x; i < a.width; i += blockDim.x) s += xb[i] * xb[i];
+  for (int i = threadIdx.x; i < a.width; i += blockDim.x) s += xb(i) * xb(i);
   s = wave_total(s);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
   __syncthreads();
   const float scale = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)a.width + a.epsilon);
   for (int i = threadIdx.x; i < a.width_p; i += blockDim.x)
-    out[i] = i < a.width ? float_to_half(xb[i] * scale * batch_weight<kMixed>(a.weights, w_norm, i)) : 0;
+    out[half_index(b, i, a.width_p)] = i < a.width ? float_to_half(xb(i) * scale * batch_weight<kMixed>(a.weights, w_norm, i)) : 0;
 }
 
 // Final RMSNorm (cast in mixed mode) and score of every stream (src/cuda/Runtime.cu:380-383;
@@ -673,14 +754,19 @@ template <int P>
 __global__ __launch_bounds__(64) void batch_final(const BatchArgs* __restrict__ ap) {
   const BatchArgs& a = *ap;
   const int b = blockIdx.x, lane = threadIdx.x;
-  const float* xb = a.x + (size_t)b * a.width_p;
+  const float* x = a.x;
+  auto xb = [&](int i) { return x[act_index<P>(b, i, a.width_p)]; };
+  // Unrolled so that the loads of several iterations are in flight together (the sums keep
+  // their order).
   float s = 0.f;
-  for (int i = lane; i < a.width; i += 64) s += xb[i] * xb[i];
+#pragma unroll 8
+  for (int i = lane; i < a.width; i += 64) s += xb(i) * xb(i);
   const float scale = 1.0f / sqrtf(wave_total(s) / (float)a.width + a.epsilon);
   float acc = 0.f;
+#pragma unroll 8
   for (int i = lane; i < a.width; i += 64) {
     const float wn = batch_weight<P>(a.weights, a.w_final_norm, i), ws = batch_weight<P>(a.weights, a.w_score, i);
-    acc += ws * cast<P>(xb[i] * scale * wn);
+    acc += ws * cast<P>(xb(i) * scale * wn);
   }
   acc = wave_total(acc);
   if (lane == 0) {

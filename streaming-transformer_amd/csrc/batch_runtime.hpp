@@ -38,6 +38,7 @@ class Batch : public BatchBase {
   template <int P, int E, bool kNorm, int CT, int SW>
   void project(const void* X, int ld, uint32_t woff, int N, uint32_t norm, int layer, int max_tiles = kGroupTiles);
   int group_tiles(int cols, int max_tiles) const;
+  void stage_events(const float* inputs, float* block) const;
   bool wide_qkv_ = false, wide_gateup_ = false;  // two column tiles per workgroup
   size_t block_words_ = 0;  // one (layer, stream) block [H][W][dh] of the K (or V) ring, in 4-byte words
   void launch() {
@@ -88,12 +89,13 @@ Batch::Batch(const st_config& config, bool mixed, const st_tensor* tensors, size
     throw Error(ST_ERR_DEVICE, std::string("Supported target is gfx950; found ") + prop.gcnArchName);
   HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
 
-  // Weight arena: the single-stream layout (rows padded to 1 KiB slabs).
+  // Weight arena: the single-stream runtime's (rows padded to 1 KiB slabs), with the
+  // projection matrices in MFMA operand order (tiled).
   const int slab = 1024 / (prec_ == kFp32 ? 4 : 2);
   offsets_.width_p = round_up(c_.width, slab);
   offsets_.ffn_p = round_up(c_.ffn, slab);
   offsets_.features_p = round_up(c_.features, slab);
-  build_arena(c_, prec_, tensors, count, offsets_, weights_);
+  build_arena(c_, prec_, tensors, count, offsets_, weights_, true);
 
   BatchArgs& a = args_;
   a.streams = streams_;
@@ -178,17 +180,13 @@ int Batch::group_tiles(int cols, int max_tiles) const {
 
 template <int P, int E, bool kNorm, int CT, int SW>
 void Batch::project(const void* X, int ld, uint32_t woff, int N, uint32_t norm, int layer, int max_tiles) {
-  const int nt = group_tiles(N / (kBatchTile * CT), max_tiles);
-  const dim3 grid(N / (kBatchTile * CT), streams_p_ / kBatchTile / nt), block(64 * kSlices / SW);
-  if (nt == 4)
-    hipLaunchKernelGGL((batch_proj<P, E, kNorm, 4, CT, SW>), grid, block, 0, stream_, dargs_, X, ld, woff, ld, N, ld,
-                       norm, layer);
-  else if (nt == 2)
-    hipLaunchKernelGGL((batch_proj<P, E, kNorm, 2, CT, SW>), grid, block, 0, stream_, dargs_, X, ld, woff, ld, N, ld,
-                       norm, layer);
-  else
-    hipLaunchKernelGGL((batch_proj<P, E, kNorm, 1, CT, SW>), grid, block, 0, stream_, dargs_, X, ld, woff, ld, N, ld,
-                       norm, layer);
+  const int cols = N / (kBatchTile * CT);
+  const int nt = group_tiles(cols, max_tiles);
+  const dim3 grid(cols, streams_p_ / kBatchTile / nt), block(64 * kSlices / SW);
+  auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, stream_, dargs_, X, woff, N, ld, norm, layer); };
+  if (nt == 4) go(batch_proj<P, E, kNorm, 4, CT, SW>);
+  else if (nt == 2) go(batch_proj<P, E, kNorm, 2, CT, SW>);
+  else go(batch_proj<P, E, kNorm, 1, CT, SW>);
 }
 
 // Workgroup shapes per projection. Every shape computes the same fixed slice tree, so the
@@ -252,11 +250,24 @@ void Batch::launch_sequence() {
   HIP_CHECK(hipGetLastError());
 }
 
+// The events of one step into the padded input block in the projections' operand layout.
+// Four consecutive columns from a multiple of 4 are consecutive in the layout.
+void Batch::stage_events(const float* inputs, float* block) const {
+  const int fp = args_.features_p;
+  auto at = [&](int b, int k) { return prec_ == kBf16w ? act_index<kBf16w>(b, k, fp) : act_index<kFp32>(b, k, fp); };
+  for (int b = 0; b < streams_; b++) {
+    const float* src = inputs + (size_t)b * c_.features;
+    int k = 0;
+    for (; k + 4 <= c_.features; k += 4) std::memcpy(block + at(b, k), src + k, 16);
+    for (; k < c_.features; k++) block[at(b, k)] = src[k];
+  }
+}
+
 void Batch::step(const float* inputs, float* scores) {
   if (!inputs || !scores) throw Error(ST_ERR_INVALID, "Null argument");
   const int fp = args_.features_p;
   float* h = reinterpret_cast<float*>(host_in_.ptr);
-  for (int b = 0; b < streams_; b++) std::memcpy(h + (size_t)b * fp, inputs + (size_t)b * c_.features, (size_t)c_.features * 4);
+  stage_events(inputs, h);
   HIP_CHECK(hipMemcpyAsync(args_.in, host_in_.ptr, (size_t)streams_p_ * fp * 4, hipMemcpyHostToDevice, stream_));
   replay();
   HIP_CHECK(hipMemcpyAsync(host_out_.ptr, args_.score, (size_t)streams_ * 4, hipMemcpyDeviceToHost, stream_));
@@ -308,9 +319,7 @@ double Batch::device_run(const float* inputs, size_t count, double* per_step) {
     throw Error(ST_ERR_INVALID, "Invalid trace (empty, or more than 4 GiB of padded inputs)");
   std::vector<float> padded(count * (size_t)streams_p_ * fp, 0.f);
   for (size_t i = 0; i < count; i++)
-    for (int b = 0; b < streams_; b++)
-      std::memcpy(&padded[(i * streams_p_ + b) * fp], inputs + (i * streams_ + b) * c_.features,
-                  (size_t)c_.features * 4);
+    stage_events(inputs + i * streams_ * c_.features, &padded[i * streams_p_ * fp]);
   DeviceBuffer dev;
   dev.alloc(padded.size() * 4);
   HIP_CHECK(hipMemcpy(dev.ptr, padded.data(), padded.size() * 4, hipMemcpyHostToDevice));

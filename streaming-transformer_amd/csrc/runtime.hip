@@ -668,8 +668,15 @@ int Runtime::legal_blocks_t() {
 // The weight arena (also used by the batched runtime): rows padded to whole 1 KiB slabs, q/k/v
 // stacked, gate and up rows interleaved per unit; offsets recorded in args_. The row lengths
 // args_.width_p, ffn_p and features_p must be set.
+// The weight arena. Matrices are row-major with rows padded to the slab, or, with `tiled`
+// (the batched runtime's MFMA projections), in operand order: 16-row tiles, then blocks of KB
+// columns, then the 64 lanes of an MFMA operand (row r mod 16 + 16 x column group), KB / 4
+// values each, so that a wave loads one block as one contiguous run of 64 x 16 bytes (a
+// row-major operand makes every lane's 16 bytes a separate access for the L1, whose rate of
+// accesses then bounds the projections). KB is 16 for the FP32 MFMA (FP32 weights, and the
+// mixed mode's input projection) and 32 for the 16-bit MFMAs.
 static void build_arena(const st_config& c_, int prec_, const st_tensor* tensors, size_t count, StepArgs& args_,
-                        DeviceBuffer& weights_) {
+                        DeviceBuffer& weights_, bool tiled = false) {
   std::map<std::string, const st_tensor*> byname;
   for (size_t i = 0; i < count; i++) {
     if (!tensors[i].name || !tensors[i].data) throw Error(ST_ERR_INVALID, "Null tensor");
@@ -705,11 +712,31 @@ static void build_arena(const st_config& c_, int prec_, const st_tensor* tensors
       host.push_back((unsigned char)(h >> 8));
     }
   };
-  auto put_rows = [&](const float* data, int rows, int cols, int cols_p) {
+  // Rows of `cols` values padded to `cols_p`, appended to a row-major matrix.
+  auto add_rows = [&](std::vector<float>& m, const float* data, int rows, int cols, int cols_p) {
     for (int r = 0; r < rows; r++) {
-      for (int k = 0; k < cols; k++) put(data[(size_t)r * cols + k]);
-      for (int k = cols; k < cols_p; k++) put(0.f);
+      m.insert(m.end(), data + (size_t)r * cols, data + (size_t)r * cols + cols);
+      m.insert(m.end(), (size_t)(cols_p - cols), 0.f);
     }
+  };
+  auto put_matrix = [&](const std::vector<float>& m, int cols_p, bool fp32_mfma) {
+    if (!tiled) {
+      for (float v : m) put(v);
+      return;
+    }
+    const int kb_cols = fp32_mfma ? 16 : 32, per_lane = kb_cols / 4;
+    const int rows = (int)(m.size() / cols_p);
+    for (int t = 0; t < rows / 16; t++)
+      for (int kb = 0; kb < cols_p / kb_cols; kb++)
+        for (int lane = 0; lane < 64; lane++)
+          for (int e = 0; e < per_lane; e++)
+            put(m[(size_t)(t * 16 + lane % 16) * cols_p + kb * kb_cols + lane / 16 * per_lane + e]);
+  };
+  const bool fp32_mfma = prec_ == kFp32;
+  auto put_rows = [&](const float* data, int rows, int cols, int cols_p, bool fp32) {
+    std::vector<float> m;
+    add_rows(m, data, rows, cols, cols_p);
+    put_matrix(m, cols_p, fp32);
   };
   auto put_vector = [&](const float* data, int n) {
     for (int i = 0; i < n; i++) put(data[i]);
@@ -718,7 +745,7 @@ static void build_arena(const st_config& c_, int prec_, const st_tensor* tensors
   const int d = c_.width, f = c_.ffn;
   align();
   a.w_input = (uint32_t)host.size();
-  put_rows(get("input", {d, c_.features})->data, d, c_.features, a.features_p);
+  put_rows(get("input", {d, c_.features})->data, d, c_.features, a.features_p, prec_ != kBf16w);
   for (int l = 0; l < c_.layers; l++) {
     std::string p = "layers." + std::to_string(l) + ".";
     LayerWeights& lw = a.layer[l];
@@ -730,30 +757,40 @@ static void build_arena(const st_config& c_, int prec_, const st_tensor* tensors
     put_vector(get(p + "norm2", {d})->data, d);
     align();
     lw.qkv = (uint32_t)host.size();
-    put_rows(get(p + "q", {d, d})->data, d, d, a.width_p);
-    put_rows(get(p + "k", {d, d})->data, d, d, a.width_p);
-    put_rows(get(p + "v", {d, d})->data, d, d, a.width_p);
+    {
+      std::vector<float> m;
+      for (const char* part : {"q", "k", "v"}) add_rows(m, get(p + part, {d, d})->data, d, d, a.width_p);
+      put_matrix(m, a.width_p, fp32_mfma);
+    }
     align();
     lw.out = (uint32_t)host.size();
-    put_rows(get(p + "out", {d, d})->data, d, d, a.width_p);
+    put_rows(get(p + "out", {d, d})->data, d, d, a.width_p, fp32_mfma);
     align();
     lw.gateup = (uint32_t)host.size();
     const float* gate = get(p + "gate", {f, d})->data;
     const float* up = get(p + "up", {f, d})->data;
-    for (int r = 0; r < f; r++) {
-      put_rows(gate + (size_t)r * d, 1, d, a.width_p);
-      put_rows(up + (size_t)r * d, 1, d, a.width_p);
+    {
+      std::vector<float> m;
+      for (int r = 0; r < f; r++) {
+        add_rows(m, gate + (size_t)r * d, 1, d, a.width_p);
+        add_rows(m, up + (size_t)r * d, 1, d, a.width_p);
+      }
+      put_matrix(m, a.width_p, fp32_mfma);
     }
     align();
     lw.down = (uint32_t)host.size();
-    put_rows(get(p + "down", {d, f})->data, d, f, a.ffn_p);
+    put_rows(get(p + "down", {d, f})->data, d, f, a.ffn_p, fp32_mfma);
   }
   align();
   a.w_final_norm = (uint32_t)host.size();
   put_vector(get("final_norm", {d})->data, d);
   align();
   a.w_score = (uint32_t)host.size();
-  put_rows(get("score", {1, d})->data, 1, d, a.width_p);
+  {
+    std::vector<float> m;
+    add_rows(m, get("score", {1, d})->data, 1, d, a.width_p);
+    for (float v : m) put(v);  // a vector (the final phase reads it as one)
+  }
   align();
   host.resize(host.size() + 256, 0);
   if (host.size() > (size_t)std::numeric_limits<int>::max())
