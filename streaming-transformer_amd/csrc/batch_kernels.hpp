@@ -48,6 +48,7 @@ struct BatchArgs {
 };
 
 constexpr int kSlices = 8;       // K-slices of a projection, K / 8 columns each
+constexpr size_t kInfinityCacheBytes = (size_t)256 << 20;  // MI355X's memory-side cache (MALL)
 
 // Loads from the weight arena through the global address space. The arena's base arrives in
 // the arguments block as a generic pointer, and a load through a generic (flat) pointer also
@@ -483,14 +484,20 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
 }
 
 // Four consecutive ring elements of K or V (FP32, or FP16 in mixed mode) as floats.
-template <int P>
+// Global (not flat) loads, so that they count on the vector memory counter only; kNT marks
+// them non-temporal, for rings larger than the Infinity Cache (see batch_attention).
+template <int P, bool kNT>
 __device__ __forceinline__ float4 ring4(const void* ring, size_t i) {
+  typedef const __attribute__((address_space(1))) u32x2_t g2;
+  typedef const __attribute__((address_space(1))) u32x4_t g4;
   if constexpr (P == kMixed) {
-    const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(ring) + i);
+    const void* p = reinterpret_cast<const uint16_t*>(ring) + i;
+    const uint2 h = __builtin_bit_cast(uint2, kNT ? __builtin_nontemporal_load((g2*)p) : *(g2*)p);
     return make_float4(half_to_float((unsigned short)(h.x & 0xffffu)), half_to_float((unsigned short)(h.x >> 16)),
                        half_to_float((unsigned short)(h.y & 0xffffu)), half_to_float((unsigned short)(h.y >> 16)));
   } else {
-    return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(ring) + i);
+    const void* p = reinterpret_cast<const float*>(ring) + i;
+    return __builtin_bit_cast(float4, kNT ? __builtin_nontemporal_load((g4*)p) : *(g4*)p);
   }
 }
 
@@ -501,7 +508,7 @@ constexpr int kAttnThreads = 256;  // batch_attention's workgroup: four waves, 1
 // first chunk's V loads are issued before the softmax reductions. The arithmetic is the general
 // loop's, in the same order: per row a dot product over the lane's four elements and a 16-lane
 // sum; per group the V rows of slots grp, grp + 16, ... accumulated in slot order.
-template <int P, int NP, bool kEarlyV>
+template <int P, int NP, bool kEarlyV, bool kNT>
 __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int h, int valid, size_t base,
                                                   const float* q, float div, float* pr, float* wred,
                                                   float4 (*vred)[17]) {
@@ -520,7 +527,7 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
   for (int c0 = 0; c0 < valid; c0 += kRows) {
     float4 kv[NP];
 #pragma unroll
-    for (int p = 0; p < NP; p++) kv[p] = in ? ring4<P>(a.keys, at(c0 + 16 * p + grp)) : z4;
+    for (int p = 0; p < NP; p++) kv[p] = in ? ring4<P, kNT>(a.keys, at(c0 + 16 * p + grp)) : z4;
 #pragma unroll
     for (int p = 0; p < NP; p++) {
       const int s = c0 + 16 * p + grp;
@@ -541,7 +548,7 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
   }
   if constexpr (kEarlyV) {
 #pragma unroll
-    for (int p = 0; p < NP; p++) vv[p] = in ? ring4<P>(a.values, at(16 * p + grp)) : z4;
+    for (int p = 0; p < NP; p++) vv[p] = in ? ring4<P, kNT>(a.values, at(16 * p + grp)) : z4;
   }
   mx = wave_top(mx);
   if (lane == 0) wred[wave] = mx;
@@ -562,7 +569,7 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
   for (int c0 = 0; c0 < valid; c0 += kRows) {
     if (!kEarlyV || c0 > 0) {
 #pragma unroll
-      for (int p = 0; p < NP; p++) vv[p] = in ? ring4<P>(a.values, at(c0 + 16 * p + grp)) : z4;
+      for (int p = 0; p < NP; p++) vv[p] = in ? ring4<P, kNT>(a.values, at(c0 + 16 * p + grp)) : z4;
     }
 #pragma unroll
     for (int p = 0; p < NP; p++) {
@@ -620,8 +627,13 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
 // against 8.8, at 16 streams 5.2 (8) against 7.4; with FP16 K/V the per-pass loop is faster up to
 // 64 streams (B = 1: 3.1 against 4.0 us; B = 64: 7.8 against 8.2) and four passes at 256
 // (16.4 against 17.2 us).
+// kNT: the K and V loads are non-temporal, for rings larger than the Infinity Cache: a step
+// streams them through once, and cached they would evict the weights the projections re-read
+// (Main, bfloat16 weights: 454 -> 436 us per step at 256 streams, 249 -> 241 at 64; mixed mode
+// 400 -> 382 at 256). Rings that fit stay cached from step to step instead (mixed mode at 64
+// streams: 253 against 270 us).
 enum AttnLoads : int { kAttnPerPass = 0, kAttnChunk4, kAttnChunk8, kAttnChunk4Early };
-template <int P, int kLoads>
+template <int P, int kLoads, bool kNT>
 __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs* __restrict__ ap, int layer) {
   const BatchArgs& a = *ap;
   extern __shared__ float pr[];
@@ -637,7 +649,7 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
   const float div = sqrtf((float)dim);
   if constexpr (kLoads != kAttnPerPass) {
     constexpr int np = kLoads == kAttnChunk8 ? 8 : 4;
-    attention_chunked<P, np, kLoads == kAttnChunk4Early>(a, b, h, valid, base, q, div, pr, wred, vred);
+    attention_chunked<P, np, kLoads == kAttnChunk4Early, kNT>(a, b, h, valid, base, q, div, pr, wred, vred);
     return;
   }
   float mx = -INFINITY;
@@ -649,7 +661,7 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
     const size_t row = base + (size_t)(s < valid ? s : valid - 1) * dim;
     float dot = 0.f;
     for (int d = 4 * r; d < dim; d += 64) {
-      const float4 kv = ring4<P>(a.keys, row + d);
+      const float4 kv = ring4<P, kNT>(a.keys, row + d);
       const float4 qv = *reinterpret_cast<const float4*>(q + d);
       dot += qv.x * kv.x;
       dot += qv.y * kv.y;
@@ -685,7 +697,7 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
 #pragma unroll 4
       for (int s = grp; s < valid; s += 16) {
         const float p = pr[s];
-        const float4 vv = ring4<P>(a.values, base + (size_t)s * dim + d);
+        const float4 vv = ring4<P, kNT>(a.values, base + (size_t)s * dim + d);
         o.x += p * vv.x;
         o.y += p * vv.y;
         o.z += p * vv.z;

@@ -210,6 +210,8 @@ void Batch::launch_sequence() {
   const int attn_loads = dim_ > 64 ? kAttnPerPass
                          : P == kMixed ? (streams_p_ >= 256 ? kAttnChunk4 : kAttnPerPass)
                          : streams_p_ <= 32 ? kAttnChunk8 : streams_p_ == 64 ? kAttnChunk4Early : kAttnChunk4;
+  // K/V rings larger than the Infinity Cache are read with non-temporal loads.
+  const bool kv_nt = 2 * c_.layers * (size_t)streams_ * block_words_ * 4 > kInfinityCacheBytes;
   // Mixed mode casts each norm's output, so its norms run first into xn; the other modes fold
   // the norm into the projection (kNorm).
   constexpr bool kFold = P != kMixed;
@@ -228,14 +230,19 @@ void Batch::launch_sequence() {
     {
       const dim3 grid(streams_ * c_.heads), block(kAttnThreads);
       const size_t lds = (size_t)c_.window * 4;
-      if (attn_loads == kAttnChunk4)
-        hipLaunchKernelGGL((batch_attention<P, kAttnChunk4>), grid, block, lds, stream_, dargs_, l);
-      else if (attn_loads == kAttnChunk8)
-        hipLaunchKernelGGL((batch_attention<P, kAttnChunk8>), grid, block, lds, stream_, dargs_, l);
-      else if (attn_loads == kAttnChunk4Early)
-        hipLaunchKernelGGL((batch_attention<P, kAttnChunk4Early>), grid, block, lds, stream_, dargs_, l);
-      else
-        hipLaunchKernelGGL((batch_attention<P, kAttnPerPass>), grid, block, lds, stream_, dargs_, l);
+      auto attend = [&](auto nt) {
+        constexpr bool kNT = decltype(nt)::value;
+        if (attn_loads == kAttnChunk4)
+          hipLaunchKernelGGL((batch_attention<P, kAttnChunk4, kNT>), grid, block, lds, stream_, dargs_, l);
+        else if (attn_loads == kAttnChunk8)
+          hipLaunchKernelGGL((batch_attention<P, kAttnChunk8, kNT>), grid, block, lds, stream_, dargs_, l);
+        else if (attn_loads == kAttnChunk4Early)
+          hipLaunchKernelGGL((batch_attention<P, kAttnChunk4Early, kNT>), grid, block, lds, stream_, dargs_, l);
+        else
+          hipLaunchKernelGGL((batch_attention<P, kAttnPerPass, kNT>), grid, block, lds, stream_, dargs_, l);
+      };
+      if (kv_nt) attend(std::true_type{});
+      else attend(std::false_type{});
     }
     if (narrow) project<P, kEpOut, false, 2, 1>(a.attn, a.width_p, w.out, d, 0u, l);
     else project<P, kEpOut, false, 1, 1>(a.attn, a.width_p, w.out, d, 0u, l);
