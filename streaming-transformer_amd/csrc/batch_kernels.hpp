@@ -627,11 +627,11 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
 // against 8.8, at 16 streams 5.2 (8) against 7.4; with FP16 K/V the per-pass loop is faster up to
 // 64 streams (B = 1: 3.1 against 4.0 us; B = 64: 7.8 against 8.2) and four passes at 256
 // (16.4 against 17.2 us).
-// kNT: the K and V loads are non-temporal, for rings larger than the Infinity Cache: a step
-// streams them through once, and cached they would evict the weights the projections re-read
-// (Main, bfloat16 weights: 454 -> 436 us per step at 256 streams, 249 -> 241 at 64; mixed mode
-// 400 -> 382 at 256). Rings that fit stay cached from step to step instead (mixed mode at 64
-// streams: 253 against 270 us).
+// kNT: the K and V loads are non-temporal, for rings that do not fit in the Infinity Cache
+// beside the weights: a step streams them through once, and cached they would evict the
+// weights the projections re-read (Main, bfloat16 weights: 454 -> 436 us per step at 256
+// streams, 249 -> 241 at 64; mixed mode 400 -> 382 at 256). Rings that fit stay cached from
+// step to step instead (mixed mode at 64 streams: 253 against 270 us).
 enum AttnLoads : int { kAttnPerPass = 0, kAttnChunk4, kAttnChunk8, kAttnChunk4Early };
 template <int P, int kLoads, bool kNT>
 __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs* __restrict__ ap, int layer) {

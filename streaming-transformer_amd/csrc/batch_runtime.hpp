@@ -210,8 +210,9 @@ void Batch::launch_sequence() {
   const int attn_loads = dim_ > 64 ? kAttnPerPass
                          : P == kMixed ? (streams_p_ >= 256 ? kAttnChunk4 : kAttnPerPass)
                          : streams_p_ <= 32 ? kAttnChunk8 : streams_p_ == 64 ? kAttnChunk4Early : kAttnChunk4;
-  // K/V rings larger than the Infinity Cache are read with non-temporal loads.
-  const bool kv_nt = 2 * c_.layers * (size_t)streams_ * block_words_ * 4 > kInfinityCacheBytes;
+  // K/V rings that do not fit in the Infinity Cache beside the weights are read with
+  // non-temporal loads, so that the weights stay cached.
+  const bool kv_nt = 2 * c_.layers * (size_t)streams_ * block_words_ * 4 + offsets_.weight_bytes > kInfinityCacheBytes;
   // Mixed mode casts each norm's output, so its norms run first into xn; the other modes fold
   // the norm into the projection (kNorm).
   constexpr bool kFold = P != kMixed;
