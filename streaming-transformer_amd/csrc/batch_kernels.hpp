@@ -184,7 +184,10 @@ __device__ __forceinline__ void k_loop(int first, int slice, Load&& load, Pin&& 
 // and are bit-identical for every batch size. The padded batch is a multiple of NT tiles, so
 // the loops have no branches. X and W are in the tiled operand layout (act_index and the tiled
 // arena): one 16 x KB block of either is 64 lanes' contiguous 16-byte pieces in lane order.
-// X is the padded buffer of K columns; W the N x K matrix at arena offset `woff`.
+// X is the padded buffer of K columns; W the N x K matrix at offset `woff` of the arena
+// `weights`. What the K loop's first loads need (the arena, X, the shape) comes in the kernel
+// arguments, not from the arguments block, whose read would add a memory round trip before
+// them.
 // FP32 weights: v_mfma_f32_16x16x4_f32, k block of 16; lane l supplies A[l % 16][l / 16] and
 // B[l / 16][l % 16], register r of lane l holds D[4 (l / 16) + r][l % 16]; the four MFMA
 // steps use k = kb + 4 (l / 16) + c for step c, the same index for A and B.
@@ -198,8 +201,9 @@ __device__ __forceinline__ void k_loop(int first, int slice, Load&& load, Pin&& 
 // 1 / sqrt(sum / d + eps).
 template <int P, int E, bool kNorm, int NT, int CT, int SW>
 __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs* __restrict__ ap,
+                                                               const char* __restrict__ weights,
                                                                const void* __restrict__ X, uint32_t woff, int N,
-                                                               int K, uint32_t w_norm, int layer) {
+                                                               int K, int width, uint32_t w_norm, int layer) {
   constexpr int kWaves = kSlices / SW;
   const BatchArgs& a = *ap;
   __shared__ float red[kWaves][NT][CT][16][17];
@@ -208,7 +212,7 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
   const int n0 = blockIdx.x * kBatchTile * CT;
   const int t0 = blockIdx.y * NT;
   const int r16 = lane & 15, g = lane >> 4;
-  const int slice = K / kSlices, width = a.width;
+  const int slice = K / kSlices;
   const int first = wave * SW;  // the wave's first slice
   f4v acc[SW][NT][CT];
   float ss[SW][NT];
@@ -227,8 +231,8 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
     // Tiled operands: block (tile, k / 16) holds 64 lanes x 4 values.
     const int nkb = K / 16;
     const float* xr = reinterpret_cast<const float*>(X) + ((size_t)t0 * nkb * 64 + lane) * 4;
-    const char* wr = a.weights + woff + ((size_t)(n0 / kBatchTile) * nkb * 64 + lane) * 4 * (P == kFp32 ? 4 : 2);
-    const float* gr = reinterpret_cast<const float*>(a.weights + w_norm) + 4 * g;
+    const char* wr = weights + woff + ((size_t)(n0 / kBatchTile) * nkb * 64 + lane) * 4 * (P == kFp32 ? 4 : 2);
+    const float* gr = reinterpret_cast<const float*>(weights + w_norm) + 4 * g;
     struct Frag {
       float4 w[CT], gn, x[NT];
     };
@@ -288,8 +292,8 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
     // two planes of 64 lanes x 4 floats.
     const int nkb = K / 32;
     const float* xr = reinterpret_cast<const float*>(X) + ((size_t)t0 * nkb * 128 + lane) * 4;
-    const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.weights + woff) + ((size_t)(n0 / kBatchTile) * nkb * 64 + lane) * 8;
-    const uint16_t* gr = reinterpret_cast<const uint16_t*>(a.weights + w_norm) + 8 * g;
+    const uint16_t* wr = reinterpret_cast<const uint16_t*>(weights + woff) + ((size_t)(n0 / kBatchTile) * nkb * 64 + lane) * 8;
+    const uint16_t* gr = reinterpret_cast<const uint16_t*>(weights + w_norm) + 8 * g;
     struct Frag {
       uint4 w[CT], gn;
       float4 xlo[NT], xhi[NT];
@@ -359,7 +363,7 @@ __global__ __launch_bounds__(64 * kSlices / SW) void batch_proj(const BatchArgs*
     // Tiled operands: block (tile, k / 32) holds 64 lanes x 8 values.
     const int nkb = K / 32;
     const uint16_t* xr = reinterpret_cast<const uint16_t*>(X) + ((size_t)t0 * nkb * 64 + lane) * 8;
-    const uint16_t* wr = reinterpret_cast<const uint16_t*>(a.weights + woff) + ((size_t)(n0 / kBatchTile) * nkb * 64 + lane) * 8;
+    const uint16_t* wr = reinterpret_cast<const uint16_t*>(weights + woff) + ((size_t)(n0 / kBatchTile) * nkb * 64 + lane) * 8;
     struct Frag {
       uint4 w[CT], x[NT];
     };
@@ -739,7 +743,7 @@ __device__ __forceinline__ float batch_weight(const char* w, uint32_t off, int i
 // Mixed mode: RMSNorm of every stream's x into xn with the output cast to FP16
 // (src/cuda/Primitives.cuh:122-135); padding columns and padding streams are zero. One
 // workgroup of 256 threads per row of the padded batch.
-__global__ __launch_bounds__(256) void batch_norm_mixed(const BatchArgs* __restrict__ ap, uint32_t w_norm) {
+static __global__ __launch_bounds__(256) void batch_norm_mixed(const BatchArgs* __restrict__ ap, uint32_t w_norm) {
   const BatchArgs& a = *ap;
   __shared__ float red[4];
   const int b = blockIdx.x;
@@ -790,7 +794,7 @@ __global__ __launch_bounds__(64) void batch_final(const BatchArgs* __restrict__ 
 // Zero the state of stream `stream` (every stream when negative): K/V rows, hidden, position.
 // `block_words` is one (layer, stream) block of the K (or V) ring, [H][W][dh], in 4-byte words;
 // a stream's K/V is one such block in each layer (the rings are layer-major).
-__global__ void batch_reset(const BatchArgs* __restrict__ ap, int stream, size_t block_words) {
+static __global__ void batch_reset(const BatchArgs* __restrict__ ap, int stream, size_t block_words) {
   const BatchArgs& a = *ap;
   const int b0 = stream < 0 ? 0 : stream, b1 = stream < 0 ? a.streams : stream + 1;
   const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x, step = (size_t)gridDim.x * blockDim.x;

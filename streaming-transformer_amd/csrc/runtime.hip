@@ -5,7 +5,8 @@
 // device-held position and epoch. Mirrors Stream::Runtime::Impl (src/cuda/Runtime.cu:167-653) behind a C ABI.
 #include "step_phases.hpp"
 #include "mailbox.hpp"
-#include "batch_kernels.hpp"
+#include "host_common.hpp"
+#include "batch_api.hpp"
 #include "diag_kernels.hpp"
 #include "../../include/st_runtime.h"
 
@@ -32,112 +33,6 @@
 namespace stamd {
 
 static thread_local std::string g_last_error;
-
-struct Error : std::runtime_error {
-  int code;
-  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
-};
-
-#define HIP_CHECK(expr)                                                                    \
-  do {                                                                                     \
-    hipError_t _e = (expr);                                                                \
-    if (_e != hipSuccess)                                                                  \
-      throw Error(ST_ERR_DEVICE, std::string(#expr) + ": " + hipGetErrorString(_e));       \
-  } while (0)
-
-// ---------------------------------------------------------------------------------------------
-// host-side rounding (round to nearest even), matching the device conversions
-
-static uint16_t host_half_bits(float value) {
-  uint32_t u;
-  std::memcpy(&u, &value, 4);
-  uint32_t sign = (u >> 16) & 0x8000u, exp = (u >> 23) & 0xffu, man = u & 0x7fffffu;
-  if (exp == 0xffu) return (uint16_t)(sign | 0x7c00u | (man ? (0x200u | (man >> 13)) : 0u));
-  int e = (int)exp - 127 + 15;
-  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
-  if (e <= 0) {
-    if (e < -10) return (uint16_t)sign;
-    uint32_t full = man | 0x800000u;
-    int shift = 14 - e;
-    uint32_t half = full >> shift, rem = full & ((1u << shift) - 1u), mid = 1u << (shift - 1);
-    if (rem > mid || (rem == mid && (half & 1u))) half++;
-    return (uint16_t)(sign | half);
-  }
-  uint32_t half = ((uint32_t)e << 10) | (man >> 13), rem = man & 0x1fffu;
-  if (rem > 0x1000u || (rem == 0x1000u && (half & 1u))) half++;
-  return (uint16_t)(sign | half);
-}
-
-static float host_half_to_float(uint16_t bits) {
-  uint32_t sign = ((uint32_t)bits & 0x8000u) << 16, exp = (bits >> 10) & 0x1fu, man = bits & 0x3ffu;
-  uint32_t u;
-  if (exp == 0x1fu) u = sign | 0x7f800000u | (man << 13);
-  else if (exp == 0) {
-    if (!man) u = sign;
-    else {
-      float f = (float)man * 5.9604644775390625e-8f;
-      return sign ? -f : f;
-    }
-  } else u = sign | ((exp + 112u) << 23) | (man << 13);
-  float f;
-  std::memcpy(&f, &u, 4);
-  return f;
-}
-
-static uint16_t host_bf16_bits(float value) {
-  uint32_t u;
-  std::memcpy(&u, &value, 4);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
-static int round_up(int v, int m) { return (v + m - 1) / m * m; }
-
-// ---------------------------------------------------------------------------------------------
-
-struct DeviceBuffer {
-  void* ptr = nullptr;
-  size_t bytes = 0;
-  void alloc(size_t n) {
-    bytes = n;
-    HIP_CHECK(hipMalloc(&ptr, std::max<size_t>(n, 256)));
-  }
-  ~DeviceBuffer() {
-    if (ptr) (void)hipFree(ptr);
-  }
-};
-
-struct PinnedBuffer {
-  void* ptr = nullptr;
-  void alloc(size_t n) { HIP_CHECK(hipHostMalloc(&ptr, std::max<size_t>(n, 64), hipHostMallocDefault)); }
-  ~PinnedBuffer() {
-    if (ptr) (void)hipHostFree(ptr);
-  }
-};
-
-// Coherent pinned host memory mapped into the device's address space (the persistent
-// backend's mailbox and event buffer).
-struct MappedBuffer {
-  void* ptr = nullptr;
-  void* dev = nullptr;
-  void alloc(size_t n) {
-    HIP_CHECK(hipHostMalloc(&ptr, std::max<size_t>(n, 64), hipHostMallocMapped | hipHostMallocCoherent));
-    std::memset(ptr, 0, std::max<size_t>(n, 64));
-    HIP_CHECK(hipHostGetDevicePointer(&dev, ptr, 0));
-  }
-  ~MappedBuffer() {
-    if (ptr) (void)hipHostFree(ptr);
-  }
-};
-
-static void validate_config(const st_config& c) {
-  if (c.layers < 1 || c.layers > 16 || c.width < 1 || c.width > 1024 || c.heads < 1 ||
-      c.width % c.heads || (c.width / c.heads) % 2 || c.ffn < 1 || c.ffn > 4096 || c.window < 1 ||
-      c.window > 4096 || c.features < 1 || c.features > 1024 || !std::isfinite(c.epsilon) ||
-      c.epsilon <= 0)
-    throw Error(ST_ERR_INVALID, "Invalid or unsupported model dimensions");
-}
 
 static std::string json_escape(const std::string& s) {
   std::string o;
@@ -675,8 +570,8 @@ int Runtime::legal_blocks_t() {
 // row-major operand makes every lane's 16 bytes a separate access for the L1, whose rate of
 // accesses then bounds the projections). KB is 16 for the FP32 MFMA (FP32 weights, and the
 // mixed mode's input projection) and 32 for the 16-bit MFMAs.
-static void build_arena(const st_config& c_, int prec_, const st_tensor* tensors, size_t count, StepArgs& args_,
-                        DeviceBuffer& weights_, bool tiled = false) {
+void build_arena(const st_config& c_, int prec_, const st_tensor* tensors, size_t count, StepArgs& args_,
+                 DeviceBuffer& weights_, bool tiled) {
   std::map<std::string, const st_tensor*> byname;
   for (size_t i = 0; i < count; i++) {
     if (!tensors[i].name || !tensors[i].data) throw Error(ST_ERR_INVALID, "Null tensor");

@@ -8,14 +8,21 @@ import sys
 from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent.parent
-SOURCES = [PACKAGE_DIR / 'csrc' / 'runtime.hip']
+SOURCES = [PACKAGE_DIR / 'csrc' / 'runtime.hip', PACKAGE_DIR / 'csrc' / 'batch.hip']
 DEPENDS = SOURCES + list((PACKAGE_DIR / 'csrc').glob('*.hpp')) + [PACKAGE_DIR.parent / 'include' / 'st_runtime.h']
 OUTPUT = PACKAGE_DIR / 'lib' / 'libstamd.so'
 
-HIPCC_FLAGS = [
-    '-O3', '--offload-arch=gfx950', '-std=c++17', '-fPIC', '-shared', '-fno-strict-aliasing',
+COMPILE_FLAGS = [
+    '-O3', '--offload-arch=gfx950', '-std=c++17', '-fPIC', '-fno-strict-aliasing',
     # keep packed-FP32 VALU instructions out of the generated code
     '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+]
+# Per translation unit: the batched phase kernels take their arguments preloaded into SGPRs
+# (their first loads then wait for no argument load); the fused single-stream kernel is faster
+# without, so runtime.hip keeps the default.
+UNIT_FLAGS = {'batch.hip': ['-mllvm', '-amdgpu-kernarg-preload-count=16']}
+LINK_FLAGS = [
+    '--offload-arch=gfx950', '-fPIC', '-shared',
     # rocBLAS for the vendor GEMV backends
     '-L/opt/rocm/lib', '-lrocblas', '-Wl,-rpath,/opt/rocm/lib',
 ]
@@ -65,14 +72,30 @@ def build(force: bool = True, verbose: bool = False) -> Path:
         if OUTPUT.stat().st_mtime >= newest:
             return OUTPUT
     OUTPUT.parent.mkdir(parents=True, exist_ok=True)
-    tmp = OUTPUT.with_suffix('.so.tmp')
-    cmd = [hipcc(), *HIPCC_FLAGS, '-o', str(tmp), *map(str, SOURCES)]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f'hipcc failed ({proc.returncode}):\n{proc.stderr[-4000:]}')
-    if verbose:
-        sys.stderr.write(proc.stderr)
-    os.replace(tmp, OUTPUT)
+    # The translation units compile in parallel, each to an object beside the library.
+    objects = [OUTPUT.parent / (src.stem + '.o.tmp') for src in SOURCES]
+    procs = [subprocess.Popen([hipcc(), *COMPILE_FLAGS, *UNIT_FLAGS.get(src.name, []), '-c', '-o', str(obj), str(src)],
+                              stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+             for src, obj in zip(SOURCES, objects)]
+    try:
+        for src, proc in zip(SOURCES, procs):
+            _, err = proc.communicate()
+            if proc.returncode != 0:
+                raise RuntimeError(f'hipcc failed on {src.name} ({proc.returncode}):\n{err[-4000:]}')
+            if verbose:
+                sys.stderr.write(err)
+        tmp = OUTPUT.with_suffix('.so.tmp')
+        cmd = [hipcc(), *LINK_FLAGS, '-o', str(tmp), *map(str, objects)]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f'hipcc link failed ({proc.returncode}):\n{proc.stderr[-4000:]}')
+        os.replace(tmp, OUTPUT)
+    finally:
+        for p in procs:
+            if p.poll() is None:
+                p.kill()
+        for obj in objects:
+            obj.unlink(missing_ok=True)
     return OUTPUT
 
 
