@@ -166,7 +166,7 @@ void Batch::launch_sequence() {
   // FP16 K/V only from 256 streams.
   const int attn_loads = dim_ > 64 ? kAttnPerPass
                          : P == kMixed ? (streams_p_ >= 256 ? kAttnChunk4 : kAttnPerPass)
-                         : streams_p_ <= 32 ? kAttnChunk8 : streams_p_ == 64 ? kAttnChunk4Early : kAttnChunk4;
+                         : streams_p_ <= 32 ? kAttnChunk8Early : streams_p_ == 64 ? kAttnChunk4Early : kAttnChunk4;
   // K/V rings that do not fit in the Infinity Cache beside the weights are read with
   // non-temporal loads, so that the weights stay cached.
   const bool kv_nt = 2 * c_.layers * (size_t)streams_ * block_words_ * 4 + offsets_.weight_bytes > kInfinityCacheBytes;
@@ -192,10 +192,10 @@ void Batch::launch_sequence() {
         constexpr bool kNT = decltype(nt)::value;
         if (attn_loads == kAttnChunk4)
           hipLaunchKernelGGL((batch_attention<P, kAttnChunk4, kNT>), grid, block, lds, stream_, dargs_, l);
-        else if (attn_loads == kAttnChunk8)
-          hipLaunchKernelGGL((batch_attention<P, kAttnChunk8, kNT>), grid, block, lds, stream_, dargs_, l);
         else if (attn_loads == kAttnChunk4Early)
           hipLaunchKernelGGL((batch_attention<P, kAttnChunk4Early, kNT>), grid, block, lds, stream_, dargs_, l);
+        else if (attn_loads == kAttnChunk8Early)
+          hipLaunchKernelGGL((batch_attention<P, kAttnChunk8Early, kNT>), grid, block, lds, stream_, dargs_, l);
         else
           hipLaunchKernelGGL((batch_attention<P, kAttnPerPass, kNT>), grid, block, lds, stream_, dargs_, l);
       };

@@ -624,11 +624,13 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
 // loops, on the host, by storage and batch size; every form computes the same values in the same
 // order, so a stream's bits do not depend on it:
 //  - kAttnPerPass: the general loop below, one pass of 16 rows after the other (any dh);
-//  - kAttnChunk4 / kAttnChunk8: dh <= 64, the loads of 4 or 8 passes issued together
-//    (attention_chunked), kAttnChunk4Early with the first V chunk loaded before the softmax.
+//  - kAttnChunk4, kAttnChunk4Early, kAttnChunk8Early: dh <= 64, the loads of 4 or 8 passes
+//    issued together (attention_chunked); the Early forms load the first V chunk before the
+//    softmax.
 // Measured on Main (one layer, W = 128): with FP32 K/V at 256 streams 23.2 us against 26.2 us
 // for the per-pass loop in the former stream-major layout, at 64 streams 6.95 (4, early V)
-// against 8.8, at 16 streams 5.2 (8) against 7.4; with FP16 K/V the per-pass loop is faster up to
+// against 8.8, at 16 streams 5.2 (8) against 7.4 (and 8 with early V, once the K/V loads were
+// global loads, 183.7 -> 181.2 us per Main step); with FP16 K/V the per-pass loop is faster up to
 // 64 streams (B = 1: 3.1 against 4.0 us; B = 64: 7.8 against 8.2) and four passes at 256
 // (16.4 against 17.2 us).
 // kNT: the K and V loads are non-temporal, for rings that do not fit in the Infinity Cache
@@ -636,7 +638,7 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
 // weights the projections re-read (Main, bfloat16 weights: 454 -> 436 us per step at 256
 // streams, 249 -> 241 at 64; mixed mode 400 -> 382 at 256). Rings that fit stay cached from
 // step to step instead (mixed mode at 64 streams: 253 against 270 us).
-enum AttnLoads : int { kAttnPerPass = 0, kAttnChunk4, kAttnChunk8, kAttnChunk4Early };
+enum AttnLoads : int { kAttnPerPass = 0, kAttnChunk4, kAttnChunk4Early, kAttnChunk8Early };
 template <int P, int kLoads, bool kNT>
 __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs* __restrict__ ap, int layer) {
   const BatchArgs& a = *ap;
@@ -652,8 +654,9 @@ __global__ __launch_bounds__(kAttnThreads) void batch_attention(const BatchArgs*
   const float* q = a.q + (size_t)b * a.width + h * dim;
   const float div = sqrtf((float)dim);
   if constexpr (kLoads != kAttnPerPass) {
-    constexpr int np = kLoads == kAttnChunk8 ? 8 : 4;
-    attention_chunked<P, np, kLoads == kAttnChunk4Early, kNT>(a, b, h, valid, base, q, div, pr, wred, vred);
+    constexpr int np = kLoads == kAttnChunk8Early ? 8 : 4;
+    attention_chunked<P, np, kLoads == kAttnChunk4Early || kLoads == kAttnChunk8Early, kNT>(a, b, h, valid, base, q,
+                                                                                            div, pr, wred, vred);
     return;
   }
   float mx = -INFINITY;
