@@ -745,7 +745,9 @@ __device__ __forceinline__ float batch_weight(const char* w, uint32_t off, int i
 
 // Mixed mode: RMSNorm of every stream's x into xn with the output cast to FP16
 // (src/cuda/Primitives.cuh:122-135); padding columns and padding streams are zero. One
-// workgroup of 256 threads per row of the padded batch.
+// workgroup of 256 threads per row of the padded batch. Every load (x and the norm vector,
+// at most 4 columns per thread) is issued before the reduction, so the kernel waits one
+// memory round trip; the sums keep their order.
 static __global__ __launch_bounds__(256) void batch_norm_mixed(const BatchArgs* __restrict__ ap, uint32_t w_norm) {
   const BatchArgs& a = *ap;
   __shared__ float red[4];
@@ -757,14 +759,27 @@ static __global__ __launch_bounds__(256) void batch_norm_mixed(const BatchArgs* 
     for (int i = threadIdx.x; i < a.width_p; i += blockDim.x) out[half_index(b, i, a.width_p)] = 0;
     return;
   }
+  constexpr int kPer = kMaxDim / 256;
+  float xv[kPer], gv[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; j++) {
+    const int i = threadIdx.x + 256 * j;
+    xv[j] = i < a.width ? xb(i) : 0.f;
+    gv[j] = i < a.width ? batch_weight<kMixed>(a.weights, w_norm, i) : 0.f;
+  }
   float s = 0.f;
-  for (int i = threadIdx.x; i < a.width; i += blockDim.x) s += xb(i) * xb(i);
+#pragma unroll
+  for (int j = 0; j < kPer; j++)
+    if (threadIdx.x + 256 * j < a.width) s += xv[j] * xv[j];
   s = wave_total(s);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
   __syncthreads();
   const float scale = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)a.width + a.epsilon);
-  for (int i = threadIdx.x; i < a.width_p; i += blockDim.x)
-    out[half_index(b, i, a.width_p)] = i < a.width ? float_to_half(xb(i) * scale * batch_weight<kMixed>(a.weights, w_norm, i)) : 0;
+#pragma unroll
+  for (int j = 0; j < kPer; j++) {
+    const int i = threadIdx.x + 256 * j;
+    if (i < a.width_p) out[half_index(b, i, a.width_p)] = i < a.width ? float_to_half(xv[j] * scale * gv[j]) : 0;
+  }
 }
 
 // Final RMSNorm (cast in mixed mode) and score of every stream (src/cuda/Runtime.cu:380-383;
