@@ -185,21 +185,22 @@ def test_reset_one_and_all_and_device_run_equals_stepping():
         np.testing.assert_array_equal(rt.step(events[-1]), stepped[-1])
 
 
-@pytest.mark.parametrize('streams', [64, 256])
-def test_large_rings_read_non_temporally_match_a_batch_of_one(streams):
-    # Main with bfloat16 weights: from 64 streams the K/V rings and the weights exceed the
-    # Infinity Cache, and attention reads K/V with non-temporal loads (and other loop forms);
-    # a batch of one reads them with ordinary loads. Scores and state must agree bit for bit.
+@pytest.mark.parametrize('weights,streams', [(WeightStorage.BF16, 64), (WeightStorage.BF16, 256),
+                                             (WeightStorage.AS_MODEL, 64)])
+def test_large_rings_read_non_temporally_match_a_batch_of_one(weights, streams):
+    # Main with FP32 K/V: from 64 streams the K/V rings and the weights exceed the Infinity
+    # Cache, and attention reads K/V with non-temporal loads (and other loop forms); a batch of
+    # one reads them with ordinary loads. Scores and state must agree bit for bit.
     c = SHAPES['main']
     w = synthetic_checkpoint(c, seed=17)
     steps = 36
     events = _events(c, 17, steps, streams)
     picks = (0, streams // 2, streams - 1)
-    with batch((c, w, False), streams, WeightStorage.BF16) as rt:
+    with batch((c, w, False), streams, weights) as rt:
         many = np.stack([rt.step(events[i]) for i in range(steps)])
         states = [rt.snapshot(b) for b in picks]
     for b, state in zip(picks, states):
-        with batch((c, w, False), 1, WeightStorage.BF16) as one:
+        with batch((c, w, False), 1, weights) as one:
             alone = np.array([one.step(events[i, b:b + 1])[0] for i in range(steps)], dtype=np.float32)
             np.testing.assert_array_equal(alone, many[:, b])
             ref = one.snapshot(0)
