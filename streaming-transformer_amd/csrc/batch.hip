@@ -162,10 +162,9 @@ void Batch::launch_sequence() {
   const int d = c_.width, F = c_.ffn;
   const bool wide = streams_p_ >= 64, narrow = streams_p_ >= 128 && (c_.width / kBatchTile) % 2 == 0;
   const bool huge = P != kFp32 && streams_p_ >= 256;
-  // The attention loops' form (batch_attention): chunked loads for FP32 K/V with dh <= 64; for
-  // FP16 K/V only from 256 streams.
+  // The attention loops' form (batch_attention): chunked loads for dh <= 64, eight passes with
+  // V loaded early up to 32 streams, four with V early at 64, four from 128.
   const int attn_loads = dim_ > 64 ? kAttnPerPass
-                         : P == kMixed ? (streams_p_ >= 256 ? kAttnChunk4 : kAttnPerPass)
                          : streams_p_ <= 32 ? kAttnChunk8Early : streams_p_ == 64 ? kAttnChunk4Early : kAttnChunk4;
   // K/V rings that do not fit in the Infinity Cache beside the weights are read with
   // non-temporal loads, so that the weights stay cached.

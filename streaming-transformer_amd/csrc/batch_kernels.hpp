@@ -14,6 +14,8 @@
 
 #include "step_device.hpp"
 
+#include <type_traits>
+
 namespace stamd {
 
 constexpr int kBatchMax = 256;   // streams per batch (16 batch tiles of 16 in the GEMM)
@@ -505,6 +507,28 @@ __device__ __forceinline__ float4 ring4(const void* ring, size_t i) {
   }
 }
 
+// Four consecutive ring elements as loaded (FP16 pairs in mixed mode), and their FP32 values.
+// The chunked attention keeps the loaded form in registers and widens at each use, so that the
+// FP16 values feed mixed-precision FMAs directly (widening is exact, the results unchanged).
+template <int P>
+using RingRaw = std::conditional_t<P == kMixed, uint2, float4>;
+template <int P, bool kNT>
+__device__ __forceinline__ RingRaw<P> ring_raw(const void* ring, size_t i) {
+  typedef const __attribute__((address_space(1))) u32x2_t g2;
+  typedef const __attribute__((address_space(1))) u32x4_t g4;
+  if constexpr (P == kMixed) {
+    const void* p = reinterpret_cast<const uint16_t*>(ring) + i;
+    return __builtin_bit_cast(uint2, kNT ? __builtin_nontemporal_load((g2*)p) : *(g2*)p);
+  } else {
+    return ring4<P, kNT>(ring, i);
+  }
+}
+__device__ __forceinline__ const float4& widen(const float4& v) { return v; }
+__device__ __forceinline__ float4 widen(uint2 h) {
+  return make_float4(half_to_float((unsigned short)(h.x & 0xffffu)), half_to_float((unsigned short)(h.x >> 16)),
+                     half_to_float((unsigned short)(h.y & 0xffffu)), half_to_float((unsigned short)(h.y >> 16)));
+}
+
 constexpr int kAttnThreads = 256;  // batch_attention's workgroup: four waves, 16 groups of 16 lanes
 
 // batch_attention for dh <= 64: lane (group grp, r) holds elements 4r .. 4r + 3 of its rows,
@@ -526,21 +550,24 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
   // Slots past `valid` load slot valid - 1 and are dropped.
   auto at = [&](int s) { return base + (size_t)(s < valid ? s : valid - 1) * dim + d; };
   // V rows of a chunk; filled in place (an array filled through a lambda went to scratch).
-  float4 vv[NP];
+  // K and V stay in their loaded form (RingRaw) until used.
+  const RingRaw<P> zr{};
+  RingRaw<P> vv[NP];
   float mx = -INFINITY;
   for (int c0 = 0; c0 < valid; c0 += kRows) {
-    float4 kv[NP];
+    RingRaw<P> kv[NP];
 #pragma unroll
-    for (int p = 0; p < NP; p++) kv[p] = in ? ring4<P, kNT>(a.keys, at(c0 + 16 * p + grp)) : z4;
+    for (int p = 0; p < NP; p++) kv[p] = in ? ring_raw<P, kNT>(a.keys, at(c0 + 16 * p + grp)) : zr;
 #pragma unroll
     for (int p = 0; p < NP; p++) {
       const int s = c0 + 16 * p + grp;
       float dot = 0.f;
       if (in) {
-        dot += qv.x * kv[p].x;
-        dot += qv.y * kv[p].y;
-        dot += qv.z * kv[p].z;
-        dot += qv.w * kv[p].w;
+        const float4& k = widen(kv[p]);
+        dot += qv.x * k.x;
+        dot += qv.y * k.y;
+        dot += qv.z * k.z;
+        dot += qv.w * k.w;
       }
       dot = group_sum(dot, 16);
       if (s < valid) {
@@ -552,7 +579,7 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
   }
   if constexpr (kEarlyV) {
 #pragma unroll
-    for (int p = 0; p < NP; p++) vv[p] = in ? ring4<P, kNT>(a.values, at(16 * p + grp)) : z4;
+    for (int p = 0; p < NP; p++) vv[p] = in ? ring_raw<P, kNT>(a.values, at(16 * p + grp)) : zr;
   }
   mx = wave_top(mx);
   if (lane == 0) wred[wave] = mx;
@@ -573,17 +600,18 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
   for (int c0 = 0; c0 < valid; c0 += kRows) {
     if (!kEarlyV || c0 > 0) {
 #pragma unroll
-      for (int p = 0; p < NP; p++) vv[p] = in ? ring4<P, kNT>(a.values, at(c0 + 16 * p + grp)) : z4;
+      for (int p = 0; p < NP; p++) vv[p] = in ? ring_raw<P, kNT>(a.values, at(c0 + 16 * p + grp)) : zr;
     }
 #pragma unroll
     for (int p = 0; p < NP; p++) {
       const int s = c0 + 16 * p + grp;
       if (s < valid) {
         const float pp = pr[s];
-        o.x += pp * vv[p].x;
-        o.y += pp * vv[p].y;
-        o.z += pp * vv[p].z;
-        o.w += pp * vv[p].w;
+        const float4& v = widen(vv[p]);
+        o.x += pp * v.x;
+        o.y += pp * v.y;
+        o.z += pp * v.z;
+        o.w += pp * v.w;
       }
     }
   }
@@ -630,9 +658,11 @@ __device__ __forceinline__ void attention_chunked(const BatchArgs& a, int b, int
 // Measured on Main (one layer, W = 128): with FP32 K/V at 256 streams 23.2 us against 26.2 us
 // for the per-pass loop in the former stream-major layout, at 64 streams 6.95 (4, early V)
 // against 8.8, at 16 streams 5.2 (8) against 7.4 (and 8 with early V, once the K/V loads were
-// global loads, 183.7 -> 181.2 us per Main step); with FP16 K/V the per-pass loop is faster up to
-// 64 streams (B = 1: 3.1 against 4.0 us; B = 64: 7.8 against 8.2) and four passes at 256
-// (16.4 against 17.2 us).
+// global loads, 183.7 -> 181.2 us per Main step). FP16 K/V take the same forms since the
+// chunked loops keep K and V in their loaded form (RingRaw) until each use: converted when
+// loaded, they were slower than the per-pass loop below 256 streams (at 16 streams 9.7-10.4
+// against 7.9 us per layer); kept as loaded, Main mixed steps went 204 -> 187 us at one stream,
+// 214 -> 200 at 16, 237 -> 226 at 64 and 368 -> 344 at 256.
 // kNT: the K and V loads are non-temporal, for rings that do not fit in the Infinity Cache
 // beside the weights: a step streams them through once, and cached they would evict the
 // weights the projections re-read (Main, bfloat16 weights: 454 -> 436 us per step at 256

@@ -97,8 +97,8 @@ def test_bf16_weights_match_oracle_on_rounded_weights():
     (WeightStorage.AS_MODEL, False, 40, 70), (WeightStorage.BF16, False, 40, 70), (WeightStorage.AS_MODEL, True, 40, 70),
     # 130 streams: the large-batch workgroup shapes of every projection
     (WeightStorage.BF16, False, 130, 20), (WeightStorage.AS_MODEL, True, 130, 20),
-    # 256 streams: mixed mode's attention switches to chunked loads (against the per-pass loop
-    # of a batch of one), past the window
+    # 256 streams: mixed mode's attention takes four passes of loads (against eight passes with
+    # V loaded early for a batch of one), past the window
     (WeightStorage.AS_MODEL, True, 256, 70)])
 def test_stream_independent_of_batch(weight_dtype, mixed, streams, steps):
     c = SHAPES['small']
@@ -118,7 +118,8 @@ def test_stream_independent_of_batch(weight_dtype, mixed, streams, steps):
             np.testing.assert_array_equal(x, y)
 
 
-@pytest.mark.parametrize('name,streams,steps', [('main', 16, 40), ('small', 19, 90)])
+# head dim 128: mixed mode's attention through the per-pass loop
+@pytest.mark.parametrize('name,streams,steps', [('main', 16, 40), ('small', 19, 90), ('dh128', 6, 60)])
 def test_mixed_streams_meet_the_reference_policy(name, streams, steps):
     # Mixed mode: FP16 weights and K/V with the reference's cast points; each stream against
     # the mixed oracle under the reference's numerical policy v3 (include/Numerical.hpp).
