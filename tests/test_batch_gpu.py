@@ -30,6 +30,8 @@ SHAPES = {
     'dh48': ModelConfig(2, 96, 2, 192, 40, 96),
     # head dim 128: attention's general per-pass loop (two 64-element passes per row)
     'dh128': ModelConfig(2, 256, 2, 512, 48, 256),
+    # Large's width and FFN (d = 1024, F = 4096): the longest K-slices and the widest operands
+    'wide': ModelConfig(2, 1024, 16, 4096, 40, 1024),
 }
 
 
@@ -56,6 +58,7 @@ def _check_state(state, oracle_state):
     ('dh48', 3, 60, {1: 41}),
     ('dh128', 5, 60, {2: 30}),
     ('main', 16, 24, {5: 11}),
+    ('wide', 3, 48, {1: 20}),
 ])
 def test_every_stream_matches_oracle(name, streams, steps, resets):
     c = SHAPES[name]
@@ -76,11 +79,11 @@ def test_every_stream_matches_oracle(name, streams, steps, resets):
             _check_state(rt.snapshot(b), oracles[b].snapshot())
 
 
-def test_bf16_weights_match_oracle_on_rounded_weights():
-    c = SHAPES['main']
+@pytest.mark.parametrize('name,streams,steps', [('main', 16, 20), ('wide', 5, 16)])
+def test_bf16_weights_match_oracle_on_rounded_weights(name, streams, steps):
+    c = SHAPES[name]
     w = synthetic_checkpoint(c, seed=12)
     rounded = {k: round_bf16(v) for k, v in w.items()}
-    streams, steps = 16, 20
     events = _events(c, 12, steps, streams)
     oracles = [Oracle(c, rounded, accumulate='double', threads=8) for _ in range(streams)]
     with batch((c, w, False), streams, WeightStorage.BF16) as rt:
@@ -89,7 +92,7 @@ def test_bf16_weights_match_oracle_on_rounded_weights():
             for b in range(streams):
                 ref = oracles[b].step(events[i, b])
                 assert numerical.fp32_strict_failures([got[b]], [ref], **STRICT) == 0, (i, b, got[b], ref)
-        for b in (0, 9, 15):
+        for b in (0, streams // 2, streams - 1):
             _check_state(rt.snapshot(b), oracles[b].snapshot())
 
 
@@ -119,7 +122,8 @@ def test_stream_independent_of_batch(weight_dtype, mixed, streams, steps):
 
 
 # head dim 128: mixed mode's attention through the per-pass loop
-@pytest.mark.parametrize('name,streams,steps', [('main', 16, 40), ('small', 19, 90), ('dh128', 6, 60)])
+@pytest.mark.parametrize('name,streams,steps', [('main', 16, 40), ('small', 19, 90), ('dh128', 6, 60),
+                                                ('wide', 3, 48)])
 def test_mixed_streams_meet_the_reference_policy(name, streams, steps):
     # Mixed mode: FP16 weights and K/V with the reference's cast points; each stream against
     # the mixed oracle under the reference's numerical policy v3 (include/Numerical.hpp).
@@ -132,8 +136,9 @@ def test_mixed_streams_meet_the_reference_policy(name, streams, steps):
     with batch((c, w, True), streams) as rt:
         for i in range(steps):
             if i == steps // 2:
-                rt.reset(3)
-                oracles[3].reset()
+                r = min(3, streams - 1)
+                rt.reset(r)
+                oracles[r].reset()
             scores[i] = rt.step(events[i])
             refs[i] = [o.step(events[i, b]) for b, o in enumerate(oracles)]
         for b in range(streams):
