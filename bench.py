@@ -7,10 +7,10 @@ projection, 12 layers, final norm and score, with the K/V rings carried on the G
 
 Timing: the window is first filled (W-1 events) and warmed (--warmup events), untimed;
 then exactly --steps full-window steps run through the fused backend, one fused-kernel
-launch per step, with a HIP event recorded on the runtime's stream after each launch
-(st_runtime_device_run). `value` is the p50 of those per-step device durations (inputs
-already resident in HBM). The library synchronizes its stream before and after the timed
-launches. One JSON line is printed.
+launch per step, with a timing-only HIP event (no system-scope fence) recorded on the
+runtime's stream after each launch (st_runtime_device_run). `value` is the p50 of those
+per-step device durations (inputs already resident in HBM). The library synchronizes its
+stream before and after the timed launches. One JSON line is printed.
 
 Self-check ("self_check" in the line): the state the timed launches leave (position, K/V rings,
 hidden state) and the score of the next event are compared with the C oracle's after the same

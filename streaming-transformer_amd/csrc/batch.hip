@@ -288,7 +288,7 @@ double Batch::device_run(const float* inputs, size_t count, double* per_step) {
   dev.alloc(padded.size() * 4);
   HIP_CHECK(hipMemcpy(dev.ptr, padded.data(), padded.size() * 4, hipMemcpyHostToDevice));
   std::vector<hipEvent_t> ev(count + 1);
-  for (auto& e : ev) HIP_CHECK(hipEventCreate(&e));
+  for (auto& e : ev) create_timing_event(&e);
   sync();
   HIP_CHECK(hipEventRecord(ev[0], stream_));
   for (size_t i = 0; i < count; i++) {

@@ -152,7 +152,7 @@ double ResidentBatch::device_run(const float* inputs, size_t count, double* per_
   dev.alloc(padded.size() * 4);
   HIP_CHECK(hipMemcpy(dev.ptr, padded.data(), padded.size() * 4, hipMemcpyHostToDevice));
   std::vector<hipEvent_t> ev(count + 1);
-  for (auto& e : ev) HIP_CHECK(hipEventCreate(&e));
+  for (auto& e : ev) create_timing_event(&e);
   HIP_CHECK(hipStreamSynchronize(stream_));
   HIP_CHECK(hipEventRecord(ev[0], stream_));
   for (size_t i = 0; i < count; i++) {

@@ -30,6 +30,12 @@ struct Error : std::runtime_error {
       throw Error(ST_ERR_DEVICE, std::string(#expr) + ": " + hipGetErrorString(_e));       \
   } while (0)
 
+// Events that only time device work between launches. Recorded without the system-scope
+// fence (an L2 writeback and invalidation before every record), so consecutive steps run as they
+// would untimed; the host reads results only after synchronizing the stream, which releases at
+// system scope. Measured on Large FP32: 305.0 -> 303.1 us per step.
+inline void create_timing_event(hipEvent_t* e) { HIP_CHECK(hipEventCreateWithFlags(e, hipEventDisableSystemFence)); }
+
 // ---------------------------------------------------------------------------------------------
 // host-side rounding (round to nearest even), matching the device conversions
 

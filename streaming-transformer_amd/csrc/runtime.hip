@@ -1017,7 +1017,7 @@ double Runtime::device_trace(const float* inputs, size_t count, double* per_even
     mean = (double)(st[count] - st[0]) * 1000.0 / wall_khz_ / count;
   } else {
     std::vector<hipEvent_t> ev(count + 1);
-    for (auto& e : ev) HIP_CHECK(hipEventCreate(&e));
+    for (auto& e : ev) create_timing_event(&e);
     HIP_CHECK(hipEventRecord(ev[0], stream_));
     for (size_t i = 0; i < count; i++) {
       HIP_CHECK(hipMemcpyAsync(args_.scratch + args_.s_input, reinterpret_cast<float*>(trace.ptr) + i * fp,
@@ -1103,7 +1103,7 @@ double Runtime::device_run(const float* inputs, size_t count, bool reset_first, 
   if (reset_first) reset();
   if (tagged_steps()) reserve_epochs(count);
   std::vector<hipEvent_t> ev(count + 1);
-  for (auto& e : ev) HIP_CHECK(hipEventCreate(&e));
+  for (auto& e : ev) create_timing_event(&e);
   const float* base = reinterpret_cast<const float*>(trace.ptr);
   HIP_CHECK(hipEventRecord(ev[0], stream_));
   for (size_t i = 0; i < count; i++) {
