@@ -42,7 +42,7 @@ Batch::Batch(const st_config& config, bool mixed, const st_tensor* tensors, size
   HIP_CHECK(hipGetDeviceProperties(&prop, device));
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     throw Error(ST_ERR_DEVICE, std::string("Supported target is gfx950; found ") + prop.gcnArchName);
-  HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  stream_.create();
 
   // Weight arena: the single-stream runtime's (rows padded to 1 KiB slabs), with the
   // projection matrices in MFMA operand order (tiled).
@@ -112,15 +112,12 @@ Batch::Batch(const st_config& config, bool mixed, const st_tensor* tensors, size
   reset(-1);
   HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
   launch();
-  HIP_CHECK(hipStreamEndCapture(stream_, &graph_));
-  HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+  HIP_CHECK(hipStreamEndCapture(stream_, &graph_.g));
+  graph_exec_.instantiate(graph_);
 }
 
 Batch::~Batch() {
-  if (stream_) (void)hipStreamSynchronize(stream_);
-  if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
-  if (graph_) (void)hipGraphDestroy(graph_);
-  if (stream_) (void)hipStreamDestroy(stream_);
+  if (stream_) (void)hipStreamSynchronize(stream_);  // before the buffers are freed
 }
 
 // Batch tiles per projection workgroup: the largest of 4, 2, 1 that still gives at least 256
@@ -308,7 +305,5 @@ double Batch::device_run(const float* inputs, size_t count, double* per_step) {
   for (auto& e : ev) (void)hipEventDestroy(e);
   return total / count;
 }
-
-// ---- resident batch
 
 }  // namespace stamd

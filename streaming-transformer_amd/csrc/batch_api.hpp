@@ -58,9 +58,9 @@ class Batch : public BatchBase {
 
   st_config c_;
   int prec_ = kFp32, streams_ = 1, streams_p_ = 16, dim_ = 0;
-  hipStream_t stream_ = nullptr;
-  hipGraph_t graph_ = nullptr;
-  hipGraphExec_t graph_exec_ = nullptr;
+  StreamHandle stream_;
+  GraphHandle graph_;
+  GraphExecHandle graph_exec_;
   DeviceBuffer weights_, keys_, values_, hidden_, position_, in_, x_, xn_, attn_, act_, q_, score_, rope_, args_dev_;
   PinnedBuffer host_in_, host_out_;
   StepArgs offsets_{};  // weight arena offsets (shared layout with the single-stream runtime)

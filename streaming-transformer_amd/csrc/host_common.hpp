@@ -122,6 +122,47 @@ struct MappedBuffer {
   }
 };
 
+// Owning stream and graph handles, so that a constructor that throws after creating them
+// (an invalid checkpoint, a failed capture) still releases them. A stream is drained before it
+// is destroyed. Declared in the order stream, graph, executable, they are destroyed in reverse.
+struct StreamHandle {
+  hipStream_t s = nullptr;
+  StreamHandle() = default;
+  StreamHandle(const StreamHandle&) = delete;
+  StreamHandle& operator=(const StreamHandle&) = delete;
+  void create() { HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking)); }
+  operator hipStream_t() const { return s; }
+  ~StreamHandle() {
+    if (s) {
+      (void)hipStreamSynchronize(s);
+      (void)hipStreamDestroy(s);
+    }
+  }
+};
+
+struct GraphHandle {
+  hipGraph_t g = nullptr;
+  GraphHandle() = default;
+  GraphHandle(const GraphHandle&) = delete;
+  GraphHandle& operator=(const GraphHandle&) = delete;
+  operator hipGraph_t() const { return g; }
+  ~GraphHandle() {
+    if (g) (void)hipGraphDestroy(g);
+  }
+};
+
+struct GraphExecHandle {
+  hipGraphExec_t e = nullptr;
+  GraphExecHandle() = default;
+  GraphExecHandle(const GraphExecHandle&) = delete;
+  GraphExecHandle& operator=(const GraphExecHandle&) = delete;
+  void instantiate(hipGraph_t g) { HIP_CHECK(hipGraphInstantiate(&e, g, nullptr, nullptr, 0)); }
+  operator hipGraphExec_t() const { return e; }
+  ~GraphExecHandle() {
+    if (e) (void)hipGraphExecDestroy(e);
+  }
+};
+
 inline void validate_config(const st_config& c) {
   if (c.layers < 1 || c.layers > 16 || c.width < 1 || c.width > 1024 || c.heads < 1 ||
       c.width % c.heads || (c.width / c.heads) % 2 || c.ffn < 1 || c.ffn > 4096 || c.window < 1 ||

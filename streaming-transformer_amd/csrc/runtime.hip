@@ -233,9 +233,9 @@ class Runtime {
   int phase_grid_ = 1;       // workgroups of a phase launch (staged sequence)
   bool phase_coop_ = false;  // phase launches are cooperative (the plain grid failed the probe)
   bool running_ = true;
-  hipStream_t stream_ = nullptr;
-  hipGraph_t graph_ = nullptr;
-  hipGraphExec_t graph_exec_ = nullptr;
+  StreamHandle stream_;
+  GraphHandle graph_;
+  GraphExecHandle graph_exec_;
   DeviceBuffer weights_, keys_, values_, scratch_, tagged_, position_, epoch_dev_, rope_, args_dev_;
   PinnedBuffer host_in_, host_out_;
   MappedBuffer mailbox_, mapped_in_, mapped_snap_, mapped_io_;
@@ -244,7 +244,7 @@ class Runtime {
   unsigned long long* scratch_ptr_ = nullptr;  // this device's trace_scratch (allocation-free trace)
   int device_ = 0;                             // the device this runtime was created on
   uint64_t runs_done_ = 0;   // RUN commands the persistent worker has completed
-  hipStream_t copy_stream_ = nullptr;
+  StreamHandle copy_stream_;
   StepArgs args_{};
   const StepArgs* dargs_ = nullptr;
   std::string probe_;
@@ -285,8 +285,8 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
   HIP_CHECK(hipDeviceGetAttribute(&wall_khz_, hipDeviceAttributeWallClockRate, device));
   device_ = device;
   scratch_ptr_ = trace_scratch_address();
-  HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
-  HIP_CHECK(hipStreamCreateWithFlags(&copy_stream_, hipStreamNonBlocking));
+  stream_.create();
+  copy_stream_.create();
 
   // ---- shape-derived layout
   StepArgs& a = args_;
@@ -465,8 +465,8 @@ Runtime::Runtime(const st_config& config, bool mixed, const st_tensor* tensors, 
     if (opt_.mapped) stage_input();
     sequence();
     if (opt_.mapped) stage_output();
-    HIP_CHECK(hipStreamEndCapture(stream_, &graph_));
-    HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+    HIP_CHECK(hipStreamEndCapture(stream_, &graph_.g));
+    graph_exec_.instantiate(graph_);
   };
   if (vendor()) {
     vendor_ = std::make_unique<VendorPath>(c_, prec_ == kMixed, args_, tensors, count, stream_);
@@ -540,11 +540,7 @@ Runtime::~Runtime() {
   } catch (...) {
   }
   if (stream_) (void)hipStreamSynchronize(stream_);
-  vendor_.reset();  // the rocBLAS handle refers to the stream
-  if (copy_stream_) (void)hipStreamDestroy(copy_stream_);
-  if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
-  if (graph_) (void)hipGraphDestroy(graph_);
-  if (stream_) (void)hipStreamDestroy(stream_);
+  vendor_.reset();  // the rocBLAS handle refers to the stream, which the members release after it
 }
 
 template <int P, int A>
