@@ -32,6 +32,8 @@ SHAPES = {
     'dh128': ModelConfig(2, 256, 2, 512, 48, 256),
     # Large's width and FFN (d = 1024, F = 4096): the longest K-slices and the widest operands
     'wide': ModelConfig(2, 1024, 16, 4096, 40, 1024),
+    # 29 features: events that are not whole 16-byte pieces, a padded input projection
+    'odd': ModelConfig(2, 64, 2, 128, 24, 29),
 }
 
 
@@ -59,6 +61,7 @@ def _check_state(state, oracle_state):
     ('dh128', 5, 60, {2: 30}),
     ('main', 16, 24, {5: 11}),
     ('wide', 3, 48, {1: 20}),
+    ('odd', 5, 60, {4: 31}),
 ])
 def test_every_stream_matches_oracle(name, streams, steps, resets):
     c = SHAPES[name]
@@ -79,7 +82,7 @@ def test_every_stream_matches_oracle(name, streams, steps, resets):
             _check_state(rt.snapshot(b), oracles[b].snapshot())
 
 
-@pytest.mark.parametrize('name,streams,steps', [('main', 16, 20), ('wide', 5, 16)])
+@pytest.mark.parametrize('name,streams,steps', [('main', 16, 20), ('wide', 5, 16), ('odd', 5, 40)])
 def test_bf16_weights_match_oracle_on_rounded_weights(name, streams, steps):
     c = SHAPES[name]
     w = synthetic_checkpoint(c, seed=12)
@@ -123,7 +126,7 @@ def test_stream_independent_of_batch(weight_dtype, mixed, streams, steps):
 
 # head dim 128: mixed mode's attention through the per-pass loop
 @pytest.mark.parametrize('name,streams,steps', [('main', 16, 40), ('small', 19, 90), ('dh128', 6, 60),
-                                                ('wide', 3, 48)])
+                                                ('wide', 3, 48), ('odd', 5, 60)])
 def test_mixed_streams_meet_the_reference_policy(name, streams, steps):
     # Mixed mode: FP16 weights and K/V with the reference's cast points; each stream against
     # the mixed oracle under the reference's numerical policy v3 (include/Numerical.hpp).
