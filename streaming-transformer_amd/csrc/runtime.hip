@@ -757,16 +757,18 @@ void Runtime::launch_compute() {
 // Mapped staging kernels (the reference's stage_input / stage_output, src/cuda/Runtime.cu:
 // 43-48): the event is read from host memory mapped into the device, the score and the
 // error word are written back there.
-__global__ void stage_input_kernel(const float* mapped, float* input, int n) {
-  for (int i = threadIdx.x; i < n; i += blockDim.x) input[i] = mapped[i];
+// The event crosses PCIe as one 16-byte load per thread: a padded row of up to 1024 floats in
+// a single round trip from host memory (n4: 16-byte pieces).
+__global__ void stage_input_kernel(const float4* mapped, float4* input, int n4) {
+  for (int i = threadIdx.x; i < n4; i += blockDim.x) input[i] = mapped[i];
 }
 __global__ void stage_output_kernel(const float* score_and_error, float* mapped) {
   if (threadIdx.x < 2) mapped[threadIdx.x] = score_and_error[threadIdx.x];
 }
 
 void Runtime::stage_input() {
-  hipLaunchKernelGGL(stage_input_kernel, dim3(1), dim3(256), 0, stream_, reinterpret_cast<const float*>(mapped_io_.dev),
-                     args_.scratch + args_.s_input, args_.features_p);
+  hipLaunchKernelGGL(stage_input_kernel, dim3(1), dim3(256), 0, stream_, reinterpret_cast<const float4*>(mapped_io_.dev),
+                     reinterpret_cast<float4*>(args_.scratch + args_.s_input), args_.features_p / 4);
   HIP_CHECK(hipGetLastError());
 }
 

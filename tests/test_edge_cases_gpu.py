@@ -377,3 +377,21 @@ def test_mapped_staging_equals_pinned_copies(backend):
     np.testing.assert_array_equal(s1, s0)
     for a, b in zip(st1, st0):
         np.testing.assert_array_equal(a, b)
+
+
+# Events of 29 features (the staged row's tail is padding): the mapped staging kernel moves the
+# padded row in 16-byte pieces; FP32 and mixed.
+@pytest.mark.parametrize('backend,mixed', [(Backend.FUSED, False), (Backend.FUSED, True), (Backend.GRAPH, True)])
+def test_mapped_staging_of_a_ragged_event(backend, mixed):
+    c = ModelConfig(2, 128, 2, 256, 20, 29)
+    w = synthetic_checkpoint(c, seed=39, mixed=mixed)
+    events = _events(c, 39, 50)
+    results = []
+    for mapped in (False, True):
+        with _runtime((c, w, mixed), backend, mapped=mapped) as rt:
+            scores = [rt.step(e) for e in events]
+            results.append((np.array(scores, np.float32), rt.snapshot()))
+    (s0, st0), (s1, st1) = results
+    np.testing.assert_array_equal(s1, s0)
+    for a, b in zip(st1, st0):
+        np.testing.assert_array_equal(a, b)
